@@ -1,0 +1,377 @@
+#!/usr/bin/env python3
+"""Benchmark of the fused ternary matmul path on one MI355X.
+
+Default workload: the 27B-scale decode-step weight sweep at batch 1 --
+64 layers x (QKV 5120->7168, o 5120->5120 (+= residual), gate+up
+5120->17408 as one swiglu launch, down 17408->5120 (+= residual)) plus the
+untied output projection 5120->248,320, every GEMV preceded by the Q8
+quantize of its input, the whole step captured in one hipGraph.
+5,952,839,680 B of packed codes + scales per step, seeded synthetic weights
+(trits p = 0.3/0.4/0.3, fp16 scales U[0.01, 0.05]) and N(0,1) activations.
+
+`value` = algorithmic bytes of one step / measured step time (weights,
+activations and outputs already resident in HBM), in GB/s.
+`roofline` = the dominant GEMV kernel's algorithmic bytes per launch over its
+average launch time, measured with HIP events on its own stream.
+`cpu_baseline` = the reference's CPU emulator GEMV (oracle/_ref, built from
+the reference sources) or the oracle port, timed on this host on a bounded
+sample of the same workload.
+
+Other workloads (--workload layer|batched|prefill) report configs 2-4 the
+same way; they are measurement aids, the default line is the sweep.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "bonsai-ternary-fast_amd")
+ORACLE = os.path.join(ROOT, "oracle")
+
+METRIC = "ternary GEMV HBM GB/s (% of 8 TB/s) at 27B shapes; implied batch-1 tok/s"
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+E, F, QKV, V, LAYERS = 5120, 17408, 7168, 248320, 64
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def align(n, a=256):
+    return (n + a - 1) // a * a
+
+
+def gemv_bytes(N, K, M, out_rw=1, nmat=1):
+    """Algorithmic bytes of one GEMV launch: weights (codes + scales) of every
+    matrix, the Q8 rows (q + d + s), the outputs (read too when added)."""
+    return nmat * (N * K // 4 + N * K // 64) + M * (K + K // 4) + 4 * M * N * out_rw
+
+
+def prep_bytes(K, M):
+    return M * (4 * K + K + K // 4)
+
+
+class Setup:
+    """Weights of every matrix of the sweep, resident in one device arena."""
+
+    def __init__(self, hip, torch, layers, seed=0):
+        self.hip, self.torch = hip, torch
+        shapes = []  # (name, layer, N, K, matrix id)
+        for l in range(layers):
+            shapes += [("qkv", l, QKV, E, 5 * l), ("o", l, E, E, 5 * l + 1), ("gate", l, F, E, 5 * l + 2),
+                       ("up", l, F, E, 5 * l + 3), ("down", l, E, F, 5 * l + 4)]
+        shapes.append(("output", layers, V, E, 5 * 64))
+        off, self.mats = 0, {}
+        for name, l, N, K, mid in shapes:
+            co = off
+            off = align(off + N * K // 4)
+            so = off
+            off = align(off + N * K // 64)
+            self.mats[(name, l)] = (N, K, mid, co, so)
+        self.arena_bytes = off
+        self.arena = torch.empty(off, dtype=torch.uint8, device="cuda")
+        base = self.arena.data_ptr()
+        maxblk = max(N * K // 128 for N, K, _, _, _ in self.mats.values())
+        stage = torch.empty(maxblk * 28, dtype=torch.uint8, device="cuda")
+        st = torch.cuda.current_stream().cuda_stream
+        t0 = time.time()
+        for (name, l), (N, K, mid, co, so) in self.mats.items():
+            nb = N * K // 128
+            hip.gen_ptq1_0(seed, mid, 0, nb, stage, st)
+            hip.launch_repack(stage, nb, base + co, base + so, st)
+        torch.cuda.synchronize()
+        self.setup_s = time.time() - t0
+        self.weight_bytes = sum(N * K // 4 + N * K // 64 for N, K, _, _, _ in self.mats.values())
+        del stage
+
+    def seg(self, name, l, y, ldy):
+        N, K, mid, co, so = self.mats[(name, l)]
+        base = self.arena.data_ptr()
+        return self.hip.GemvSeg(base + co, base + so, N, y, ldy)
+
+    def host_mat(self, name, l):
+        """(codes, scales) numpy copies of one matrix."""
+        import numpy as np
+        N, K, mid, co, so = self.mats[(name, l)]
+        codes = self.arena[co:co + N * K // 4].cpu().numpy().reshape(N, K // 4)
+        scales = self.arena[so:so + N * K // 64].cpu().numpy().view(np.uint16).reshape(N, K // 128)
+        return codes, scales
+
+
+class Step:
+    """One decode step (or M-row batch) of quantize + GEMV launches."""
+
+    def __init__(self, S: Setup, M, layers, with_output=True):
+        import numpy as np
+        hip, torch = S.hip, S.torch
+        self.S, self.M, self.layers = S, M, layers
+        rng = np.random.default_rng(0)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        self.x = dev(rng.standard_normal((M, E)).astype(np.float32))     # normed hidden state stand-in
+        self.xo = dev(rng.standard_normal((M, E)).astype(np.float32))    # attention-output stand-in
+        self.res = torch.zeros((M, E), dtype=torch.float32, device="cuda")
+        self.qkv = torch.zeros((M, QKV), dtype=torch.float32, device="cuda")
+        self.h = torch.zeros((M, F), dtype=torch.float32, device="cuda")
+        self.logits = torch.zeros((1, V), dtype=torch.float32, device="cuda") if with_output else None
+        Kmax = F
+        self.act = hip.Q8Act(torch.zeros((M, Kmax), dtype=torch.int8, device="cuda"),
+                             torch.zeros((M, Kmax // 32), dtype=torch.float32, device="cuda"),
+                             torch.zeros((M, Kmax // 32), dtype=torch.int32, device="cuda"))
+        self.with_output = with_output
+        # algorithmic bytes
+        b_gemv = {"qkv": gemv_bytes(QKV, E, M), "o": gemv_bytes(E, E, M, 2), "gateup": gemv_bytes(F, E, M, 1, 2),
+                  "down": gemv_bytes(E, F, M, 2), "output": gemv_bytes(V, E, 1)}
+        self.kind_bytes = b_gemv
+        self.gemv_bytes = layers * (b_gemv["qkv"] + b_gemv["o"] + b_gemv["gateup"] + b_gemv["down"])
+        self.prep_bytes = layers * (3 * prep_bytes(E, M) + prep_bytes(F, M))
+        if with_output:
+            self.gemv_bytes += b_gemv["output"]
+            self.prep_bytes += prep_bytes(E, 1)
+        self.total_bytes = self.gemv_bytes + self.prep_bytes
+        self.weight_bytes = layers * sum((QKV * E, E * E, 2 * F * E, E * F)) * 17 // 64
+        if with_output:
+            self.weight_bytes += V * E * 17 // 64
+        self.flops = 2 * M * layers * (QKV * E + E * E + 2 * F * E + E * F) + (2 * V * E if with_output else 0)
+
+    def prep(self, x, K, M, st):
+        self.S.hip.launch_prep(x, K, M, K, None, 0.0, None, None, 0, self.act, st)
+
+    def gemv(self, segs, K, M, mode, st):
+        self.S.hip.launch_gemv(segs, K, M, self.act, mode, st)
+
+    def layer(self, l, st):
+        S, M, G = self.S, self.M, self.S.hip.GemvMode
+        self.prep(self.x, E, M, st)
+        self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
+        self.prep(self.xo, E, M, st)
+        self.gemv([S.seg("o", l, self.res, E)], E, M, G.kAdd, st)
+        self.prep(self.x, E, M, st)
+        self.gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, G.kSwiglu, st)
+        self.prep(self.h, F, M, st)
+        self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
+
+    def run(self, st):
+        for l in range(self.layers):
+            self.layer(l, st)
+        if self.with_output:
+            self.prep(self.x, E, 1, st)
+            self.gemv([self.S.seg("output", self.layers, self.logits, V)], E, 1, self.S.hip.GemvMode.kStore, st)
+
+    def kind_launch(self, kind, l, st):
+        """One GEMV launch of a given kind (for per-kernel timing)."""
+        S, M, G = self.S, self.M, self.S.hip.GemvMode
+        if kind == "qkv":
+            self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
+        elif kind == "o":
+            self.gemv([S.seg("o", l, self.res, E)], E, M, G.kAdd, st)
+        elif kind == "gateup":
+            self.gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, G.kSwiglu, st)
+        elif kind == "down":
+            self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
+        else:
+            self.gemv([S.seg("output", self.layers, self.logits, V)], E, 1, G.kStore, st)
+
+
+def time_graph(hip, torch, fn, reps, warmup):
+    """Capture fn(stream) in one graph, replay warmup + reps times; returns ms per replay."""
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        fn(s.cuda_stream)  # eager pass (first-launch costs outside the graph)
+        s.synchronize()
+        g = hip.Graph(s)
+        with g:
+            fn(s.cuda_stream)
+        for _ in range(warmup):
+            g.launch()
+        s.synchronize()
+        e0, e1 = hip.Event(), hip.Event()
+        torch.cuda.synchronize()
+        e0.record(s)
+        for _ in range(reps):
+            g.launch()
+        e1.record(s)
+        s.synchronize()
+        ms = e0.elapsed_ms(e1) / reps
+    return ms, g
+
+
+def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
+    """The reference CPU emulator's GEMV (or the oracle port) on a bounded sample
+    of the same workload: the projections of the first layers, M rows."""
+    import numpy as np
+    sys.path.insert(0, ORACLE)
+    from btf_oracle import Oracle, Ref, have_ref
+    O = Oracle()
+    kind = "reference" if have_ref() else "port"
+    R = Ref() if kind == "reference" else None
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        threads = os.cpu_count() or 1
+    threads = max(1, min(16, threads))
+    M = step.M
+    rng = np.random.default_rng(0)
+    xe = rng.standard_normal((M, E)).astype(np.float32)
+    qe, de, se = O.quantize_rows(xe)
+    xf = rng.standard_normal((M, F)).astype(np.float32)
+    qf, df, sf = O.quantize_rows(xf)
+    total_t, total_b, layers_done = 0.0, 0, 0
+    cpu_model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    cpu_model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    l = 0
+    while total_t < budget_s and l < min(step.layers, 8):
+        mats = [(name, K) for name, K in (("qkv", E), ("o", E), ("gate", E), ("up", E), ("down", F))]
+        for name, K in mats:
+            codes, scales = S.host_mat(name, l)
+            q, d, s_ = (qe, de, se) if K == E else (qf, df, sf)
+            t0 = time.perf_counter()
+            O.quantize_rows(xe if K == E else xf)  # the Q8 quantize of the input
+            tq = time.perf_counter() - t0
+            if R is not None:
+                t, _ = R.emu_gemv_timed(codes, scales, K, q, d, s_, reps=1, threads=threads)
+            else:
+                t0 = time.perf_counter()
+                O.gemv(codes, scales, K, q, d, s_, nthreads=threads)
+                t = time.perf_counter() - t0
+            N = codes.shape[0]
+            total_t += t + tq
+            total_b += gemv_bytes(N, K, M) + prep_bytes(K, M)
+        layers_done += 1
+        l += 1
+    gbs = total_b / total_t / 1e9
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "tok_s_equiv": round(total_b / total_t / step.total_bytes, 4) if M == 1 else None,
+            "sample": f"{layers_done} layer(s) x (QKV 5120->7168, o 5120->5120, gate/up 5120->17408, "
+                      f"down 17408->5120), M={M}, each GEMV with its Q8 quantize; "
+                      f"{'reference EmuDecoder::gemv (src/emu_decoder.cpp:143-165) built from the reference sources' if kind == 'reference' else 'oracle port of EmuDecoder::gemv'}, "
+                      f"{total_t:.2f} s of CPU time; host CPU: {cpu_model}"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill"])
+    ap.add_argument("--batch", type=int, default=0, help="M for --workload batched (default 4,8,16,32 sweep)")
+    ap.add_argument("--layers", type=int, default=LAYERS)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the ternary matmul path has no "
+                                   "multi-GPU code (see DESIGN.md for how it would shard)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, PKG)
+    import btf_hip as hip
+
+    torch.cuda.set_device(0)
+    hip.kernels_init(0)
+    info = hip.device_info(0)
+    log(f"device {info['name']} {info['gcn_arch']} CUs={info['cu_count']}")
+
+    layers = args.layers if args.workload == "sweep" else (1 if args.workload == "layer" else 8)
+    t0 = time.time()
+    S = Setup(hip, torch, layers)
+    log(f"weights generated + repacked: {S.arena_bytes / 1e9:.3f} GB arena in {time.time() - t0:.2f} s")
+
+    if args.workload == "sweep":
+        step = Step(S, 1, layers)
+    elif args.workload == "layer":
+        step = Step(S, 1, 1, with_output=False)
+    elif args.workload == "batched":
+        step = Step(S, args.batch or 8, layers, with_output=False)
+    else:
+        step = Step(S, 512, layers, with_output=False)
+
+    ms, g = time_graph(hip, torch, step.run, args.steps, args.warmup)
+    log(f"step: {ms:.4f} ms ({step.total_bytes / 1e9:.4f} GB algorithmic)")
+    value = step.total_bytes / (ms / 1e3) / 1e9
+
+    # Per-kind GEMV timing: a graph of one launch per layer (distinct weights,
+    # > 256 MB working set except for a single layer) -> average per launch.
+    kinds = ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else [])
+    per = {}
+    for kind in kinds:
+        reps = 1 if kind == "output" else layers
+        fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st)) if kind == "output" else \
+             (lambda st, kind=kind: [step.kind_launch(kind, l, st) for l in range(layers)])
+        kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+        avg_us = kms * 1e3 / reps
+        b = step.kind_bytes[kind] if kind != "output" else step.kind_bytes["output"]
+        per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
+                     "launches_per_step": 1 if kind == "output" else layers}
+        log(f"  {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
+    dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
+    d = per[dom]
+    if step.M <= 32:
+        roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'})",
+                "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
+    else:
+        K_ = F if dom == "down" else E
+        N_ = {"qkv": QKV, "o": E, "gateup": 2 * F, "down": E}[dom]
+        tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
+        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                "kernel": f"{dom} GEMM (gemm_mfma_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (seeded ternary weights p=0.3/0.4/0.3, fp16 scales U[0.01,0.05], N(0,1) activations)",
+        "config": {
+            "workload": {"sweep": f"27B-scale decode-step weight sweep: {layers} x (QKV 5120->7168, o 5120->5120, "
+                                  "gate+up 5120->17408 swiglu, down 17408->5120) + output 5120->248320, "
+                                  "batch 1, Q8 quantize before every GEMV, one hipGraph",
+                         "layer": "one decoder layer's projections at batch 1, each with its Q8 quantize",
+                         "batched": f"batched decode, M={step.M}, {layers} layers of the 27B shapes",
+                         "prefill": f"prefill M=512, {layers} layers of the 27B shapes"}[args.workload],
+            "batch": step.M,
+            "bytes_per_step": step.total_bytes,
+            "weight_bytes_per_step": step.weight_bytes,
+            "kernels_per_step": layers * 8 + (2 if step.with_output else 0),
+            "parallelism": "single GPU",
+        },
+        "frac_of_8TBs": round(value / HBM_PEAK_GBS, 4),
+        "tok_s_equiv": round(1e3 / ms, 2) if args.workload == "sweep" else None,
+        "roofline": roof,
+        "gemv_kinds": per,
+        "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},
+    }
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(S, step, args.cpu_budget)
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,309 @@
+"""Python mirror of the reference's kernel-launch API (src/cuda/kernels.cuh,
+namespace btf::cuda) over the C ABI of libbtf_hip.so (include/btf/hip_abi.h).
+
+Names, argument order and meaning follow the reference: kernels_init,
+gemv_max_nb, launch_repack, launch_prep, launch_gemv, and the Q8Act / Hx /
+GemvSeg structs and GemvMode enum. Pointers are device addresses given as
+ints or as torch tensors (their data_ptr()); `stream` is a hipStream_t handle
+as an int (e.g. torch.cuda.current_stream().cuda_stream) or None for the null
+stream. Failures raise RuntimeError with the library's message, as the
+reference launchers throw std::runtime_error.
+
+There is no fallback: importing this module fails loudly when the HIP
+library has not been built.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import enum
+import os
+from dataclasses import dataclass
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libbtf_hip.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(f"{LIB_PATH} is missing: build it with `make -C {HERE}` (hipcc, gfx950)")
+
+_lib = C.CDLL(LIB_PATH)
+
+BTF_OK, BTF_ERR_ARGS, BTF_ERR_DEVICE, BTF_ERR_LAUNCH, BTF_ERR_NOT_INIT = 0, 1, 2, 3, 4
+
+
+class _Q8Act(C.Structure):
+    _fields_ = [("q", C.c_void_p), ("d", C.c_void_p), ("s", C.c_void_p)]
+
+
+class _Hx(C.Structure):
+    _fields_ = [("block", C.c_int), ("perm_hd", C.c_int), ("perm_nk", C.c_int), ("perm_rep", C.c_int),
+                ("signs", C.c_void_p)]
+
+
+class _GemvSeg(C.Structure):
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("N", C.c_int), ("y", C.c_void_p),
+                ("ldy", C.c_int)]
+
+
+class _DeviceInfo(C.Structure):
+    _fields_ = [("cu_count", C.c_int), ("lds_bytes_per_block", C.c_int), ("max_clock_khz", C.c_int),
+                ("mem_clock_khz", C.c_int), ("mem_bus_width_bits", C.c_int), ("l2_bytes", C.c_int),
+                ("wavefront_size", C.c_int), ("arch_major", C.c_int), ("arch_minor", C.c_int),
+                ("total_mem_bytes", C.c_int64), ("name", C.c_char * 256), ("gcn_arch", C.c_char * 64)]
+
+
+def _decl(name, args, res=C.c_int):
+    f = getattr(_lib, name)
+    f.argtypes = args
+    f.restype = res
+    return f
+
+
+_vp, _i, _i64 = C.c_void_p, C.c_int, C.c_int64
+_kernels_init = _decl("btf_hip_kernels_init", [_i])
+_gemv_max_nb = _decl("btf_hip_gemv_max_nb", [_i])
+_launch_repack = _decl("btf_hip_launch_repack", [_vp, _i64, _vp, _vp, _vp])
+_launch_prep = _decl("btf_hip_launch_prep",
+                     [_vp, _i, _i, _i, _vp, C.c_float, C.POINTER(_Hx), _vp, _i, C.POINTER(_Q8Act), _vp])
+_launch_gemv = _decl("btf_hip_launch_gemv", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _i, _vp])
+_dump = _decl("btf_hip_gemv_i32_dump", [_vp, _i, _i, _i, C.POINTER(_Q8Act), _vp, _vp])
+_set_policy = _decl("btf_hip_gemv_set_policy", [_i])
+_gen = _decl("btf_hip_gen_ptq1_0", [C.c_uint64, C.c_uint64, _i64, _i64, _vp, _vp])
+_last_error = _decl("btf_hip_last_error", [], C.c_char_p)
+_device_info = _decl("btf_hip_device_info", [_i, C.POINTER(_DeviceInfo)])
+_graph_begin = _decl("btf_hip_graph_begin", [_vp])
+_graph_end = _decl("btf_hip_graph_end", [_vp, C.POINTER(C.c_void_p)])
+_graph_launch = _decl("btf_hip_graph_launch", [_vp, _vp])
+_graph_destroy = _decl("btf_hip_graph_destroy", [_vp])
+_event_create = _decl("btf_hip_event_create", [C.POINTER(C.c_void_p)])
+_event_destroy = _decl("btf_hip_event_destroy", [_vp])
+_event_record = _decl("btf_hip_event_record", [_vp, _vp])
+_event_elapsed = _decl("btf_hip_event_elapsed_ms", [C.POINTER(C.c_float), _vp, _vp])
+_host_alloc_mapped = _decl("btf_hip_host_alloc_mapped", [C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_size_t])
+_host_free = _decl("btf_hip_host_free", [_vp])
+
+#: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
+ABI_SYMBOLS = (
+    "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
+    "btf_hip_launch_gemv", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
+    "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
+    "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
+    "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
+    "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
+    "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
+    "btf_hip_graph_destroy",
+)
+
+
+class GemvMode(enum.IntEnum):
+    """src/cuda/kernels.cuh:52"""
+    kStore = 0
+    kAdd = 1
+    kSwiglu = 2
+
+
+def _addr(p) -> int | None:
+    if p is None:
+        return None
+    if isinstance(p, int):
+        return p
+    return p.data_ptr()
+
+
+def _stream(st):
+    if st is None:
+        return None
+    if isinstance(st, int):
+        return st
+    return st.cuda_stream  # torch.cuda.Stream
+
+
+def _check(rc: int):
+    if rc != BTF_OK:
+        raise RuntimeError(_last_error().decode() or f"btf_hip error {rc}")
+
+
+@dataclass
+class Q8Act:
+    """Q8_0 activations of M rows of width K (src/cuda/kernels.cuh:26-31)."""
+    q: object = None  # int8 [M][K]
+    d: object = None  # f32 [M][K/32]
+    s: object = None  # i32 [M][K/32]
+
+    def _c(self):
+        return _Q8Act(_addr(self.q), _addr(self.d), _addr(self.s))
+
+
+@dataclass
+class Hx:
+    """Input transform of a folded weight, block 0 = none (src/cuda/kernels.cuh:33-38)."""
+    block: int = 0
+    perm_hd: int = 0
+    perm_nk: int = 0
+    perm_rep: int = 0
+    signs: object = None  # f32 [n] or None
+
+    def _c(self):
+        return _Hx(self.block, self.perm_hd, self.perm_nk, self.perm_rep, _addr(self.signs))
+
+
+@dataclass
+class GemvSeg:
+    """One packed matrix and its output (src/cuda/kernels.cuh:45-51)."""
+    codes: object = None   # u8 [N][K/4]
+    scales: object = None  # u16 [N][K/128]
+    N: int = 0
+    y: object = None       # f32 [M][ldy]
+    ldy: int = 0
+
+    def _c(self):
+        return _GemvSeg(_addr(self.codes), _addr(self.scales), self.N, _addr(self.y), self.ldy)
+
+
+def kernels_init(device: int = 0) -> None:
+    """src/cuda/kernels.cuh:17"""
+    _check(_kernels_init(device))
+
+
+def gemv_max_nb(K: int) -> int:
+    """src/cuda/kernels.cuh:20"""
+    return _gemv_max_nb(K)
+
+
+def launch_repack(src, nblocks: int, codes, scales, stream=None) -> None:
+    """src/cuda/kernels.cuh:22-24: nblocks PTQ1_0 blocks -> T2 codes + scales."""
+    _check(_launch_repack(_addr(src), nblocks, _addr(codes), _addr(scales), _stream(stream)))
+
+
+def launch_prep(x, ldx: int, M: int, n: int, normw, eps: float, hx: Hx | None, xn_out, ldxn: int, a: Q8Act,
+                stream=None) -> None:
+    """src/cuda/kernels.cuh:40-43"""
+    h = (hx or Hx())._c()
+    q = a._c()
+    _check(_launch_prep(_addr(x), ldx, M, n, _addr(normw), eps, C.byref(h), _addr(xn_out), ldxn, C.byref(q),
+                        _stream(stream)))
+
+
+def launch_gemv(segs, K: int, M: int, a: Q8Act, mode: GemvMode = GemvMode.kStore, stream=None) -> None:
+    """src/cuda/kernels.cuh:53-56. `segs` is a list of 1..3 GemvSeg."""
+    arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs])
+    q = a._c()
+    _check(_launch_gemv(arr, len(segs), K, M, C.byref(q), int(mode), _stream(stream)))
+
+
+def launch_gemv_raw(segs, nseg: int, K: int, M: int, a: Q8Act, mode: int, stream=None) -> int:
+    """Unchecked variant for tests of the argument validation: returns the status code."""
+    arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs]) if segs else None
+    q = a._c()
+    return _launch_gemv(arr, nseg, K, M, C.byref(q), mode, _stream(stream))
+
+
+def launch_prep_raw(x, ldx, M, n, normw, eps, hx, xn_out, ldxn, a: Q8Act, stream=None) -> int:
+    h = (hx or Hx())._c()
+    q = a._c()
+    return _launch_prep(_addr(x), ldx, M, n, _addr(normw), eps, C.byref(h), _addr(xn_out), ldxn, C.byref(q),
+                        _stream(stream))
+
+
+def launch_repack_raw(src, nblocks, codes, scales, stream=None) -> int:
+    return _launch_repack(_addr(src), nblocks, _addr(codes), _addr(scales), _stream(stream))
+
+
+def gemv_i32_dump(codes, N: int, K: int, M: int, a: Q8Act, I_out, stream=None) -> None:
+    """Exact I[m][n][s] (int32 [M][N][K/32]) from the production GEMV kernels."""
+    q = a._c()
+    _check(_dump(_addr(codes), N, K, M, C.byref(q), _addr(I_out), _stream(stream)))
+
+
+def gemv_set_policy(mfma_min_m: int) -> int:
+    """Batches of M >= mfma_min_m use the int8-MFMA kernel; 0 = default. Returns the previous value."""
+    return _set_policy(mfma_min_m)
+
+
+def gen_ptq1_0(seed: int, mat: int, first_block: int, nblocks: int, dst, stream=None) -> None:
+    """Seeded synthetic PTQ1_0 blocks on the device (benchmark weights)."""
+    _check(_gen(seed, mat, first_block, nblocks, _addr(dst), _stream(stream)))
+
+
+def last_error() -> str:
+    return _last_error().decode()
+
+
+def device_info(device: int = 0) -> dict:
+    info = _DeviceInfo()
+    _check(_device_info(device, C.byref(info)))
+    return {f: (getattr(info, f).decode() if isinstance(getattr(info, f), bytes) else getattr(info, f))
+            for f, _ in _DeviceInfo._fields_}
+
+
+class Graph:
+    """A captured stream sequence, replayed with one launch (hipGraph)."""
+
+    def __init__(self, stream):
+        self.stream = _stream(stream)
+        self.exec = None
+
+    def __enter__(self):
+        _check(_graph_begin(self.stream))
+        return self
+
+    def __exit__(self, et, ev, tb):
+        h = C.c_void_p()
+        rc = _graph_end(self.stream, C.byref(h))
+        if et is None:
+            _check(rc)
+        self.exec = h.value
+
+    def launch(self):
+        _check(_graph_launch(self.exec, self.stream))
+
+    def __del__(self):
+        if self.exec:
+            _graph_destroy(self.exec)
+            self.exec = None
+
+
+class Event:
+    """hipEvent on an explicit stream (timing of our own launches)."""
+
+    def __init__(self):
+        h = C.c_void_p()
+        _check(_event_create(C.byref(h)))
+        self.h = h.value
+
+    def record(self, stream):
+        _check(_event_record(self.h, _stream(stream)))
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = C.c_float()
+        _check(_event_elapsed(C.byref(ms), self.h, end.h))
+        return ms.value
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _event_destroy(self.h)
+            self.h = None
+
+
+class MappedHostBuffer:
+    """Pinned, device-mapped host memory (launch_repack may read its source from it)."""
+
+    def __init__(self, nbytes: int):
+        host, dev = C.c_void_p(), C.c_void_p()
+        _check(_host_alloc_mapped(C.byref(host), C.byref(dev), nbytes))
+        self.host, self.dev, self.nbytes = host.value, dev.value, nbytes
+
+    def view(self):
+        import numpy as np
+        return np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.host))
+
+    def close(self):
+        if self.host:
+            _host_free(self.host)
+            self.host = None
+
+    def __del__(self):
+        self.close()
+
+
+def lib_path() -> str:
+    return LIB_PATH

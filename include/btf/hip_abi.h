@@ -1,0 +1,169 @@
+/*
+ * hip_abi.h -- C ABI of the MI355X (gfx950) fused ternary matmul path.
+ *
+ * This is the drop-in boundary for the reference's kernel-launch API
+ * (src/cuda/kernels.cuh, namespace btf::cuda). Every entry point below names
+ * the reference declaration it replaces. The signatures use plain pointers,
+ * sizes and an opaque stream handle; no HIP, CUDA or torch types appear, so a
+ * host written in C, C++ (include/btf/kernels.hpp), Python (ctypes) or any
+ * FFI can bind it.
+ *
+ * Conventions (as in the reference, src/cuda/kernels.cuh:3-7):
+ *  - Every pointer is caller-owned DEVICE memory unless a comment says host.
+ *    launch_repack's src may also be pinned, mapped host memory.
+ *  - Launches are asynchronous on `stream` (NULL = the device's null stream).
+ *    They allocate nothing and never synchronise, so they are legal inside
+ *    stream (graph) capture once btf_hip_kernels_init has run for the device.
+ *  - Every function returns BTF_OK (0) or an error code; the message of the
+ *    last failure on the calling thread is btf_hip_last_error(). Argument
+ *    checks run on the host before anything touches the GPU.
+ *  - M <= 0 (or nblocks <= 0) is a no-op that returns BTF_OK.
+ */
+#ifndef BTF_HIP_ABI_H
+#define BTF_HIP_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------ */
+#define BTF_OK 0
+#define BTF_ERR_ARGS 1      /* invalid arguments (checked on the host)       */
+#define BTF_ERR_DEVICE 2    /* no usable device / device query failed        */
+#define BTF_ERR_LAUNCH 3    /* the HIP runtime rejected a launch or call     */
+#define BTF_ERR_NOT_INIT 4  /* btf_hip_kernels_init was not run for device   */
+
+typedef void* btf_stream_t; /* a hipStream_t */
+
+/* ---- structs, field for field as the reference --------------------------- */
+/* Q8_0 activations of M rows of width K: src/cuda/kernels.cuh:26-31. */
+typedef struct btf_q8act {
+  int8_t* q;  /* [M][K]                                        */
+  float* d;   /* [M][K/32]  fp16 value of amax/127, held as f32 */
+  int32_t* s; /* [M][K/32]  sum of q over the block            */
+} btf_q8act;
+
+/* Input transform of a folded weight (block 0: none): src/cuda/kernels.cuh:33-38. */
+typedef struct btf_hx {
+  int block;
+  int perm_hd, perm_nk, perm_rep; /* rep > 1: tiled -> grouped gather */
+  const float* signs;             /* [n] or NULL                       */
+} btf_hx;
+
+/* One packed matrix and its output: src/cuda/kernels.cuh:45-51. */
+typedef struct btf_gemv_seg {
+  const uint8_t* codes;   /* [N][K/4]   T2 codes                  */
+  const uint16_t* scales; /* [N][K/128] fp16 bits                 */
+  int N;
+  float* y;               /* [M][ldy]                             */
+  int ldy;
+} btf_gemv_seg;
+
+/* src/cuda/kernels.cuh:52 */
+enum { BTF_GEMV_STORE = 0, BTF_GEMV_ADD = 1, BTF_GEMV_SWIGLU = 2 };
+
+/* ---- kernel-launch API (src/cuda/kernels.cuh:16-56) ---------------------- */
+
+/* Replaces btf::cuda::kernels_init (kernels.cuh:17). Queries the device's CU
+ * count and LDS size and caches them per device. Idempotent; not thread-safe
+ * against concurrent launches; call it before any capture. */
+int btf_hip_kernels_init(int device);
+
+/* Replaces btf::cuda::gemv_max_nb (kernels.cuh:20). The number of activation
+ * rows one launch serves with a single pass over the weights for width K
+ * (launch_gemv itself accepts any M). 0 if K is not a positive multiple of 128. */
+int btf_hip_gemv_max_nb(int K);
+
+/* Replaces btf::cuda::launch_repack (kernels.cuh:22-24): nblocks PTQ1_0 blocks
+ * (28 B each, 4-byte aligned, device or pinned mapped host memory) ->
+ * codes [nblocks][32 B] + scales [nblocks] (fp16 bits). */
+int btf_hip_launch_repack(const uint8_t* src, int64_t nblocks, uint8_t* codes, uint16_t* scales,
+                          btf_stream_t stream);
+
+/* Replaces btf::cuda::launch_prep (kernels.cuh:40-43): x [M][ldx] ->
+ * [RMSNorm * normw] -> tiled->grouped perm -> signs -> blockwise WHT -> Q8_0
+ * into a (dense rows of width n). normw NULL: no norm; hx NULL or
+ * hx->block == 0: no transform; xn_out (optional, [M][ldxn]) receives the
+ * normed rows. n % 32 == 0 is required. */
+int btf_hip_launch_prep(const float* x, int ldx, int M, int n, const float* normw, float eps, const btf_hx* hx,
+                        float* xn_out, int ldxn, const btf_q8act* a, btf_stream_t stream);
+
+/* Replaces btf::cuda::launch_gemv (kernels.cuh:53-56). STORE / ADD:
+ * y = W x or y += W x for each of the 1..3 segments (all share K and x).
+ * SWIGLU: segs[0] = gate, segs[1] = up (same N); segs[0].y = silu(g) * u and
+ * segs[1].y is unused. Requires K % 128 == 0. Any M >= 1. */
+int btf_hip_launch_gemv(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, int mode,
+                        btf_stream_t stream);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* btf_hip_last_error(void);
+
+/* ---- additions without a reference counterpart --------------------------- */
+
+/* Test hook: runs the same GEMV kernels as btf_hip_launch_gemv (path chosen
+ * the same way, or forced by btf_hip_gemv_set_policy) but writes the exact
+ * integer sub-block accumulators I[m][n][s] = code.q - s[m][s] as int32
+ * [M][N][K/32] instead of y. */
+int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q8act* a, int32_t* I_out,
+                          btf_stream_t stream);
+
+/* GEMV path policy: batches of M >= mfma_min_m rows run on the int8-MFMA
+ * kernel, smaller ones on the v_dot4 kernel. 0 restores the default.
+ * Process-global; for tests and benchmarks. Returns the previous value. */
+int btf_hip_gemv_set_policy(int mfma_min_m);
+
+/* Seeded synthetic PTQ1_0 blocks (the benchmark's weight generator): blocks
+ * [first_block, first_block + nblocks) of matrix `mat`, trits i.i.d. with
+ * P(-1,0,+1) = (0.3,0.4,0.3) and fp16 scales RNE(U[0.01,0.05]). dst is
+ * device memory [nblocks][28]. */
+int btf_hip_gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst,
+                       btf_stream_t stream);
+
+/* Device description for reports. name must hold name_len bytes. */
+typedef struct btf_device_info {
+  int cu_count;
+  int lds_bytes_per_block;
+  int max_clock_khz;
+  int mem_clock_khz;
+  int mem_bus_width_bits;
+  int l2_bytes;
+  int wavefront_size;
+  int arch_major, arch_minor;
+  int64_t total_mem_bytes;
+  char name[256];
+  char gcn_arch[64];
+} btf_device_info;
+int btf_hip_device_info(int device, btf_device_info* out);
+
+/* Minimal runtime helpers so host code never includes HIP headers. */
+int btf_hip_device_count(int* n);
+int btf_hip_set_device(int device);
+int btf_hip_malloc(void** p, size_t bytes);
+int btf_hip_free(void* p);
+int btf_hip_host_alloc_mapped(void** host, void** dev, size_t bytes); /* pinned, mapped */
+int btf_hip_host_free(void* host);
+int btf_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+int btf_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+int btf_hip_memset(void* dst, int value, size_t bytes);
+int btf_hip_device_synchronize(void);
+int btf_hip_stream_create(btf_stream_t* s);
+int btf_hip_stream_destroy(btf_stream_t s);
+int btf_hip_stream_synchronize(btf_stream_t s);
+typedef void* btf_event_t;
+int btf_hip_event_create(btf_event_t* e);
+int btf_hip_event_destroy(btf_event_t e);
+int btf_hip_event_record(btf_event_t e, btf_stream_t s);
+int btf_hip_event_elapsed_ms(float* ms, btf_event_t start, btf_event_t stop);
+typedef void* btf_graph_exec_t;
+int btf_hip_graph_begin(btf_stream_t s);                      /* starts stream capture */
+int btf_hip_graph_end(btf_stream_t s, btf_graph_exec_t* out); /* ends capture, instantiates */
+int btf_hip_graph_launch(btf_graph_exec_t g, btf_stream_t s);
+int btf_hip_graph_destroy(btf_graph_exec_t g);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

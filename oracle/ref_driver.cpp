@@ -1,0 +1,194 @@
+// ref_driver.cpp -- TEST INFRASTRUCTURE. Compiled by oracle/Makefile together
+// with the reference's own CPU sources, read where they lie in the reference
+// checkout (nothing is copied), into oracle/_ref/libbtf_ref.so. It exposes the
+// reference's functions through a C ABI so tests can pin the oracle
+// (btf_oracle.c) against the real code. Only tests/golden/make_golden.py and
+// the CPU tests load it; it never travels into the product library.
+//
+// EmuDecoder (src/emu_decoder.cpp) keeps gemv() and prep() private inside an
+// anonymous namespace, so this translation unit includes that source file and
+// reaches them on an emulator built from the reference's tiny synthetic model
+// (ref/bonsai-decoder/src/synth.cpp).
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <condition_variable>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <set>
+#include <sstream>
+#include <stdexcept>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "bd/cpu_ops.hpp"
+#include "bd/gguf.hpp"
+#include "bd/model.hpp"
+#include "bd/synth.hpp"
+#include "bd/types.hpp"
+#include "btf/fast.hpp"
+#include "btf/packed.hpp"
+
+#define private public
+#include "emu_decoder.cpp"
+#undef private
+
+namespace {
+
+struct RefEmu {
+  std::unique_ptr<bd::Model> model;
+  std::unique_ptr<btf::FastDecoder> dec;
+};
+
+int g_threads = 1;
+
+// The emulator on the reference's smallest synthetic model; rebuilt when the
+// requested thread count changes (its ThreadPool is sized at construction).
+RefEmu& emu() {
+  static RefEmu e;
+  static int built_threads = -1;
+  if (built_threads != g_threads) {
+    e.dec.reset();
+    if (!e.model) {
+      bd::SynthOptions so;
+      so.n_layer = 1;
+      e.model = bd::Model::from_gguf(bd::Gguf::from_memory(bd::make_synth_qwen35(so)));
+    }
+    btf::FastOptions o;
+    o.threads = g_threads;
+    o.n_ctx = 16;
+    e.dec = btf::make_emu_decoder(*e.model, o);
+    built_threads = g_threads;
+  }
+  return e;
+}
+
+btf::EmuDecoder* emu_dec() { return static_cast<btf::EmuDecoder*>(emu().dec.get()); }
+
+}  // namespace
+
+extern "C" {
+
+float ref_fp16_to_f32(uint16_t h) { return bd::fp16_to_f32(h); }
+uint16_t ref_f32_to_fp16(float f) { return bd::f32_to_fp16(f); }
+int ref_ptq1_0_trit(const uint8_t* blk, int e) { return bd::ptq1_0_trit(blk, e); }
+
+void ref_quant_ptq1_0(const float* x, uint8_t* dst, int64_t n) { bd::quant_row(bd::T_PTQ1_0, x, dst, n); }
+void ref_quant_q8_0(const float* x, uint8_t* dst, int64_t n) { bd::quant_row(bd::T_Q8_0, x, dst, n); }
+void ref_dequant_ptq1_0(const uint8_t* src, float* dst, int64_t n) { bd::dequant_row(bd::T_PTQ1_0, src, dst, n); }
+
+void ref_repack_rows(const uint8_t* src, int64_t rows, int64_t K, uint8_t* codes, uint16_t* scales) {
+  btf::repack_rows(src, rows, K, codes, scales);
+}
+int ref_packed_code(const uint8_t* row_codes, int64_t e) { return btf::packed_code(row_codes, e); }
+int ref_code_byte(int e) { return btf::code_byte(e); }
+int ref_code_shift(int e) { return btf::code_shift(e); }
+
+int ref_q8_block(const float* x, int8_t* q, float* d) { return btf::q8_block_host(x, q, d); }
+void ref_round_q8_0(const float* x, int64_t n, float* out) { bd::round_q8_0(x, n, out); }
+int ref_sub_dot(uint32_t w0, uint32_t w1, const uint32_t* aw) { return btf::sub_dot_host(w0, w1, aw); }
+float ref_silu(float x) { return bd::silu(x); }
+
+void ref_rmsnorm(const float* x, const float* w, int64_t n, float eps, float* y) { bd::rmsnorm(x, w, n, eps, y); }
+void ref_fwht(float* x, int n) { bd::fwht(x, n); }
+
+// bd::matvec_raw on a PTQ1_0 tensor [N][K] (ggml_act != 0: activations
+// rounded through round_q8_0 first), ref/bonsai-decoder/src/cpu_ops.cpp:199-221.
+void ref_matvec_ptq1_0(const uint8_t* src, int64_t N, int64_t K, const float* x, float* y, int ggml_act) {
+  bd::GgufTensor t;
+  t.name = "w";
+  t.ne = {K, N};
+  t.type = bd::T_PTQ1_0;
+  t.data = src;
+  bd::ThreadPool pool(1);
+  bd::matvec_raw(pool, t, x, y, ggml_act != 0);
+}
+
+// The emulator's GEMV (src/emu_decoder.cpp:143-165) on caller data.
+int ref_emu_gemv(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K, const int8_t* q, const float* d,
+                 const int32_t* s, int M, float* y, int64_t ldy, int add) {
+  try {
+    btf::PackedMatrix P;
+    P.N = N;
+    P.K = K;
+    P.codes.assign(codes, codes + (size_t)N * (K / 4));
+    P.scales.assign(scales, scales + (size_t)N * (K / 128));
+    btf::Q8 a;
+    a.resize(M, (int)K);
+    std::memcpy(a.q.data(), q, (size_t)M * K);
+    std::memcpy(a.d.data(), d, (size_t)M * (K / 32) * 4);
+    std::memcpy(a.s.data(), s, (size_t)M * (K / 32) * 4);
+    emu_dec()->gemv(P, a, M, y, (int)ldy, add != 0);
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "ref_emu_gemv: %s\n", e.what());
+    return -1;
+  }
+}
+
+// Threads of the emulator's ThreadPool (0 = hardware concurrency, as bd::ThreadPool).
+void ref_emu_set_threads(int n) { g_threads = n; }
+
+// The emulator's GEMV timed around the call only (steady_clock, the clock
+// EmuDecoder::step uses, src/emu_decoder.cpp:102-105); reps calls, returns the
+// total seconds or -1 on error. The packed matrix and Q8 rows are built once.
+double ref_emu_gemv_timed(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K, const int8_t* q,
+                          const float* d, const int32_t* s, int M, float* y, int64_t ldy, int add, int reps) {
+  try {
+    btf::PackedMatrix P;
+    P.N = N;
+    P.K = K;
+    P.codes.assign(codes, codes + (size_t)N * (K / 4));
+    P.scales.assign(scales, scales + (size_t)N * (K / 128));
+    btf::Q8 a;
+    a.resize(M, (int)K);
+    std::memcpy(a.q.data(), q, (size_t)M * K);
+    std::memcpy(a.d.data(), d, (size_t)M * (K / 32) * 4);
+    std::memcpy(a.s.data(), s, (size_t)M * (K / 32) * 4);
+    btf::EmuDecoder* E = emu_dec();
+    const auto t0 = std::chrono::steady_clock::now();
+    for (int r = 0; r < reps; ++r) E->gemv(P, a, M, y, (int)ldy, add != 0);
+    return std::chrono::duration<double>(std::chrono::steady_clock::now() - t0).count();
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "ref_emu_gemv_timed: %s\n", e.what());
+    return -1.0;
+  }
+}
+
+// The emulator's fused prep (src/emu_decoder.cpp:122-140) on dense rows
+// x [M][n]; block == 0 means no input transform.
+int ref_emu_prep(const float* x, int M, int n, const float* normw, float eps, int block, int perm_hd, int perm_nk,
+                 int perm_rep, const float* signs, float* xn_out, int8_t* q, float* d, int32_t* s) {
+  try {
+    std::vector<float> sg;
+    bd::HadamardXform hx;
+    hx.active = block > 0;
+    hx.block = block;
+    hx.perm_hd = perm_hd;
+    hx.perm_nk = perm_nk;
+    hx.perm_rep = perm_rep;
+    if (signs) {
+      sg.assign(signs, signs + n);
+      hx.signs = &sg;
+    }
+    btf::EmuDecoder* E = emu_dec();
+    E->d_.eps = eps;
+    btf::Q8 a;
+    E->prep(x, M, n, normw, hx, a, xn_out);
+    std::memcpy(q, a.q.data(), (size_t)M * n);
+    std::memcpy(d, a.d.data(), (size_t)M * (n / 32) * 4);
+    std::memcpy(s, a.s.data(), (size_t)M * (n / 32) * 4);
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "ref_emu_prep: %s\n", e.what());
+    return -1;
+  }
+}
+
+}  // extern "C"

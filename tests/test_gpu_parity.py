@@ -1,0 +1,362 @@
+"""GPU parity tests: every HIP kernel of the path, called through the C ABI,
+against the oracle on the same seeded inputs.
+
+Bars: bit-exact for repack (bytes), Q8 (q, d bits, s) and the int32
+sub-block accumulators I[m][n][s]; GEMV outputs within rel-RMS 1e-3 and
+max |err| <= 1e-3 * max |ref| of the emulator (src/emu_decoder.cpp:143-165).
+The shapes follow the reference's kernel tests
+(tests/test_gpu_kernels.cpp:556-564) plus the 27B layer shapes.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close_1e3, gen_mat, random_act, random_mat, random_ptq, rel_rms
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def dev(a):
+    """numpy -> device tensor with the same bytes."""
+    torch = _torch()
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    elif a.dtype == np.uint32:
+        a = a.view(np.int32)
+    return torch.from_numpy(a.copy()).cuda()
+
+
+def host(t, dtype=None):
+    torch = _torch()
+    torch.cuda.synchronize()
+    a = t.cpu().numpy()
+    return a.view(dtype) if dtype is not None else a
+
+
+def zeros(shape, dtype):
+    torch = _torch()
+    return torch.zeros(shape, dtype=dtype, device="cuda")
+
+
+def stream():
+    return _torch().cuda.current_stream().cuda_stream
+
+
+def q8_dev(q, d, s, hip):
+    return hip.Q8Act(dev(q), dev(d), dev(s))
+
+
+# ---------------------------------------------------------------- repack
+@pytest.mark.parametrize("kind", ["encoder", "random_bytes"])
+def test_repack_device_source(hip, oracle, kind):
+    rng = np.random.default_rng(1234)
+    N, K = 41, 1024
+    if kind == "encoder":
+        src = random_ptq(oracle, rng, N, K)
+    else:  # every byte value, including ones the encoder never emits
+        src = rng.integers(0, 256, (N, K // 128 * 28), dtype=np.uint8)
+    codes_ref, scales_ref = oracle.repack_rows(src, N, K)
+    torch = _torch()
+    codes = zeros((N, K // 4), torch.uint8)
+    scales = zeros((N, K // 128), torch.int16)
+    hip.launch_repack(dev(src), N * K // 128, codes, scales, stream())
+    assert np.array_equal(host(codes), codes_ref)
+    assert np.array_equal(host(scales, np.uint16), scales_ref)
+
+
+def test_repack_mapped_host_source(hip, oracle):
+    """The source may be pinned, mapped host memory (as at model load)."""
+    rng = np.random.default_rng(7)
+    N, K = 33, 2048
+    src = random_ptq(oracle, rng, N, K)
+    buf = hip.MappedHostBuffer(src.size)
+    buf.view()[:] = src.reshape(-1)
+    codes_ref, scales_ref = oracle.repack_rows(src, N, K)
+    torch = _torch()
+    codes = zeros((N, K // 4), torch.uint8)
+    scales = zeros((N, K // 128), torch.int16)
+    hip.launch_repack(buf.dev, N * K // 128, codes, scales, stream())
+    assert np.array_equal(host(codes), codes_ref)
+    assert np.array_equal(host(scales, np.uint16), scales_ref)
+    buf.close()
+
+
+def test_repack_many_blocks_ragged(hip, oracle):
+    """Grid-stride path: more blocks than one grid covers, ragged tail."""
+    nb = 1_000_003
+    src = oracle.gen_ptq1_0(3, 11, nb)
+    codes_ref, scales_ref = oracle.repack_blocks(src, nb)
+    torch = _torch()
+    codes = zeros((nb, 32), torch.uint8)
+    scales = zeros((nb,), torch.int16)
+    hip.launch_repack(dev(src), nb, codes, scales, stream())
+    assert np.array_equal(host(codes), codes_ref)
+    assert np.array_equal(host(scales, np.uint16), scales_ref)
+
+
+def test_generator_matches_oracle(hip, oracle):
+    torch = _torch()
+    for first, nb in [(0, 1000), (123_457, 777)]:
+        ref = oracle.gen_ptq1_0(0, 5, nb, first_block=first)
+        out = zeros((nb, 28), torch.uint8)
+        hip.gen_ptq1_0(0, 5, first, nb, out, stream())
+        assert np.array_equal(host(out), ref)
+
+
+# ---------------------------------------------------------------- Q8 prep
+def _special_rows(K):
+    """Rows that hit the Q8 edge cases: zero blocks (+0 / -0 last), exact .5
+    ties, +-amax, tiny values (subnormal fp16 d), large values."""
+    x = np.zeros((6, K), np.float32)
+    x[0, :32] = 0.0
+    x[0, 32:64] = -0.0
+    x[0, 64:96] = np.linspace(-1, 1, 32)
+    x[0, 95] = -0.0  # non-zero block ending in -0
+    b = np.arange(32, dtype=np.float32)
+    x[1, :32] = b - 15.5  # amax 16 -> id = 127/16, q = x*id
+    x[1, 32:64] = np.where(b % 2 == 0, 2.5, -3.5)  # with amax 127 below: id = 1 -> ties
+    x[1, 63] = 127.0
+    x[1, 64:96] = -127.0
+    x[1, 96:128] = 1e-7 * (b - 16)  # tiny: fp16 d is subnormal
+    x[2] = 1e4 * np.sin(np.arange(K, dtype=np.float32))
+    x[3] = 1e-30 * np.cos(np.arange(K, dtype=np.float32))
+    x[4, ::7] = -3.0
+    x[5] = np.float32(0.5) * (np.arange(K) % 5 - 2)
+    return x
+
+
+@pytest.mark.parametrize("K", [256, 1024, 5120, 17408])
+def test_q8_bit_exact(hip, oracle, K):
+    rng = np.random.default_rng(K)
+    M = 13
+    x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    x = np.concatenate([x, _special_rows(K)], axis=0)
+    M = x.shape[0]
+    ldx = K + 8  # row stride wider than the row
+    xp = np.zeros((M, ldx), np.float32)
+    xp[:, :K] = x
+    q_ref, d_ref, s_ref = oracle.quantize_rows(x)
+    torch = _torch()
+    a = hip.Q8Act(zeros((M, K), torch.int8), zeros((M, K // 32), torch.float32), zeros((M, K // 32), torch.int32))
+    hip.launch_prep(dev(xp), ldx, M, K, None, 0.0, None, None, 0, a, stream())
+    assert np.array_equal(host(a.q), q_ref)
+    assert np.array_equal(host(a.d).view(np.uint32), d_ref.view(np.uint32))
+    assert np.array_equal(host(a.s), s_ref)
+
+
+def test_q8_unaligned_rows(hip, oracle):
+    """Scalar-load variant: a row stride that is not a multiple of 4 floats."""
+    rng = np.random.default_rng(5)
+    M, K, ldx = 5, 1024, 1027
+    xp = (rng.standard_normal((M, ldx)) * 2).astype(np.float32)
+    q_ref, d_ref, s_ref = oracle.quantize_rows(np.ascontiguousarray(xp[:, :K]))
+    torch = _torch()
+    a = hip.Q8Act(zeros((M, K), torch.int8), zeros((M, K // 32), torch.float32), zeros((M, K // 32), torch.int32))
+    hip.launch_prep(dev(xp), ldx, M, K, None, 0.0, None, None, 0, a, stream())
+    assert np.array_equal(host(a.q), q_ref)
+    assert np.array_equal(host(a.d).view(np.uint32), d_ref.view(np.uint32))
+    assert np.array_equal(host(a.s), s_ref)
+
+
+# The reference's prep cases (tests/test_gpu_kernels.cpp:557-561):
+# (n, hadamard block, norm, perm, signs, M)
+PREP_CASES = [(1024, 64, True, False, True, 1), (5120, 1024, True, False, True, 3),
+              (2048, 128, False, True, True, 8), (256, 0, True, False, False, 2),
+              (17408, 1024, False, False, True, 1)]
+
+
+@pytest.mark.parametrize("n,block,norm,perm,signs,M", PREP_CASES)
+def test_prep_full(hip, oracle, n, block, norm, perm, signs, M):
+    rng = np.random.default_rng(1234 + n)
+    eps = 1e-6
+    x = (rng.standard_normal((M, n)) * 3).astype(np.float32)
+    w = rng.standard_normal(n).astype(np.float32)
+    sg = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float32)
+    hd, nk, rep = (32, n // 64, 2) if perm else (0, 0, 0)
+    q_ref, d_ref, s_ref, xn_ref = oracle.prep(x, w if norm else None, eps, block, hd, nk, rep,
+                                              sg if signs else None)
+    torch = _torch()
+    a = hip.Q8Act(zeros((M, n), torch.int8), zeros((M, n // 32), torch.float32), zeros((M, n // 32), torch.int32))
+    xn = zeros((M, n), torch.float32)
+    hx = hip.Hx(block, hd, nk, rep, dev(sg) if signs else None)
+    hip.launch_prep(dev(x), n, M, n, dev(w) if norm else None, eps, hx, xn, n, a, stream())
+    gq, gd, gs, gxn = host(a.q), host(a.d), host(a.s), host(xn)
+    # The reference's bars (tests/test_gpu_kernels.cpp:152-158). Without the
+    # norm every stage is order-identical, so the result is bit-exact.
+    dq = np.abs(gq.astype(np.int32) - q_ref.astype(np.int32))
+    assert dq.max() <= 1 and (dq != 0).mean() <= 1e-3
+    assert rel_rms(gd, d_ref) <= 1e-4
+    assert rel_rms(gxn, xn_ref) <= 1e-6
+    if not norm:
+        assert np.array_equal(gq, q_ref)
+        assert np.array_equal(gd.view(np.uint32), d_ref.view(np.uint32))
+        assert np.array_equal(gs, s_ref)
+        assert np.array_equal(gxn, xn_ref)
+
+
+# ---------------------------------------------------------------- GEMV / GEMM
+PATHS = {"dot4": 1 << 20, "mfma": 1}  # policy: M >= value uses MFMA
+
+
+@pytest.fixture(params=list(PATHS))
+def path(request, hip):
+    hip.gemv_set_policy(PATHS[request.param])
+    yield request.param
+    hip.gemv_set_policy(0)
+
+
+@pytest.mark.parametrize("K,M", [(1024, 1), (1024, 3), (1024, 8), (1024, 13), (5120, 1), (5120, 4),
+                                 (17408, 1), (17408, 2), (2048, 32)])
+def test_gemv_i32_bit_exact(hip, oracle, path, K, M):
+    """The int32 sub-block accumulators are bit-exact on both kernel paths."""
+    rng = np.random.default_rng(K * 31 + M)
+    N = 37
+    codes, scales = random_mat(oracle, rng, N, K)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    I_ref = oracle.gemv_i32(codes, K, q, s)
+    torch = _torch()
+    out = zeros((M, N, K // 32), torch.int32)
+    hip.gemv_i32_dump(dev(codes), N, K, M, q8_dev(q, d, s, hip), out, stream())
+    assert np.array_equal(host(out), I_ref)
+
+
+@pytest.mark.parametrize("K,M", [(1024, 1), (1024, 3), (1024, 8), (1024, 13), (5120, 1), (17408, 2)])
+def test_gemv_modes_three_segments(hip, oracle, path, K, M):
+    """store into three outputs with ldy = N + 3, add, and swiglu
+    (tests/test_gpu_kernels.cpp:203-276), against the emulator GEMV."""
+    rng = np.random.default_rng(4321 + K + M)
+    Ns = [37, 64, 9]
+    mats = [random_mat(oracle, rng, n, K) for n in Ns]
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    act = q8_dev(q, d, s, hip)
+    torch = _torch()
+    # store
+    ys = [zeros((M, n + 3), torch.float32) for n in Ns]
+    segs = [hip.GemvSeg(dev(c), dev(sc), n, y, n + 3) for (c, sc), n, y in zip(mats, Ns, ys)]
+    hip.launch_gemv(segs, K, M, act, hip.GemvMode.kStore, stream())
+    for (c, sc), n, y in zip(mats, Ns, ys):
+        ref = oracle.gemv(c, sc, K, q, d, s)
+        got = host(y)
+        assert_close_1e3(got[:, :n], ref, f"store N={n}")
+        assert np.all(got[:, n:] == 0), "wrote past N"
+    # add: y = y0 + W x
+    y0 = rng.standard_normal((M, Ns[0])).astype(np.float32)
+    yd = dev(y0)
+    hip.launch_gemv([hip.GemvSeg(dev(mats[0][0]), dev(mats[0][1]), Ns[0], yd, Ns[0])], K, M, act,
+                    hip.GemvMode.kAdd, stream())
+    ref = oracle.gemv(mats[0][0], mats[0][1], K, q, d, s, y=y0.copy(), add=True)
+    assert_close_1e3(host(yd), ref, "add")
+    # swiglu: gate = mats[1], up = a fresh N=64 matrix; segs[1].y unused (None)
+    up = random_mat(oracle, rng, Ns[1], K)
+    g = zeros((M, Ns[1]), torch.float32)
+    sw = [hip.GemvSeg(dev(mats[1][0]), dev(mats[1][1]), Ns[1], g, Ns[1]),
+          hip.GemvSeg(dev(up[0]), dev(up[1]), Ns[1], None, 0)]
+    hip.launch_gemv(sw, K, M, act, hip.GemvMode.kSwiglu, stream())
+    gref = oracle.gemv(mats[1][0], mats[1][1], K, q, d, s)
+    uref = oracle.gemv(up[0], up[1], K, q, d, s)
+    assert_close_1e3(host(g), oracle.swiglu(gref, uref), "swiglu")
+
+
+@pytest.mark.parametrize("K,N", [(5120, 5120), (5120, 7168), (17408, 5120)])
+def test_gemv_27b_shapes_batch1(hip, oracle, K, N):
+    """Config shapes at M = 1 on the seeded generator's weights."""
+    codes, scales = gen_mat(oracle, 0, N + K, N, K)
+    rng = np.random.default_rng(0)
+    _, q, d, s = random_act(oracle, rng, 1, K)
+    ref = oracle.gemv(codes, scales, K, q, d, s)
+    torch = _torch()
+    y = zeros((1, N), torch.float32)
+    hip.launch_gemv([hip.GemvSeg(dev(codes), dev(scales), N, y, N)], K, 1, q8_dev(q, d, s, hip),
+                    hip.GemvMode.kStore, stream())
+    assert_close_1e3(host(y), ref, f"{K}->{N}")
+    I_ref = oracle.gemv_i32(codes[:64], K, q, s)
+    out = zeros((1, 64, K // 32), torch.int32)
+    hip.gemv_i32_dump(dev(codes[:64].copy()), 64, K, 1, q8_dev(q, d, s, hip), out, stream())
+    assert np.array_equal(host(out), I_ref)
+
+
+@pytest.mark.parametrize("M", [4, 8, 16, 32, 512])
+def test_gemm_batched_and_prefill(hip, oracle, M):
+    """Config-3/4 batch sizes on a 5120-wide layer slice (N = 256)."""
+    K, N = 5120, 256
+    codes, scales = gen_mat(oracle, 1, 77, N, K)
+    rng = np.random.default_rng(M)
+    _, q, d, s = random_act(oracle, rng, M, K)
+    ref = oracle.gemv(codes, scales, K, q, d, s)
+    torch = _torch()
+    y = zeros((M, N), torch.float32)
+    hip.launch_gemv([hip.GemvSeg(dev(codes), dev(scales), N, y, N)], K, M, q8_dev(q, d, s, hip),
+                    hip.GemvMode.kStore, stream())
+    assert_close_1e3(host(y), ref, f"M={M}")
+
+
+def test_prep_then_gemv_end_to_end(hip, oracle):
+    """GPU quantize feeding the GPU GEMV equals oracle quantize + emulator GEMV."""
+    rng = np.random.default_rng(99)
+    K, N, M = 5120, 300, 2
+    codes, scales = random_mat(oracle, rng, N, K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    q, d, s = oracle.quantize_rows(x)
+    ref = oracle.gemv(codes, scales, K, q, d, s)
+    torch = _torch()
+    a = hip.Q8Act(zeros((M, K), torch.int8), zeros((M, K // 32), torch.float32), zeros((M, K // 32), torch.int32))
+    hip.launch_prep(dev(x), K, M, K, None, 0.0, None, None, 0, a, stream())
+    y = zeros((M, N), torch.float32)
+    hip.launch_gemv([hip.GemvSeg(dev(codes), dev(scales), N, y, N)], K, M, a, hip.GemvMode.kStore, stream())
+    assert_close_1e3(host(y), ref, "prep+gemv")
+
+
+def test_graph_replay_matches_eager(hip, oracle):
+    """A captured quantize + GEMV + add sequence replays identically (several
+    replays with eager work and syncs between them)."""
+    torch = _torch()
+    rng = np.random.default_rng(2024)
+    K, N = 1024, 200
+    codes, scales = random_mat(oracle, rng, N, K)
+    x = dev(rng.standard_normal((1, K)).astype(np.float32))
+    a = hip.Q8Act(zeros((1, K), torch.int8), zeros((1, K // 32), torch.float32), zeros((1, K // 32), torch.int32))
+    cd, sd = dev(codes), dev(scales)
+    y = zeros((1, N), torch.float32)
+    s = torch.cuda.Stream()  # the null stream cannot be captured
+    with torch.cuda.stream(s):
+        def seq():
+            hip.launch_prep(x, K, 1, K, None, 0.0, None, None, 0, a, s.cuda_stream)
+            hip.launch_gemv([hip.GemvSeg(cd, sd, N, y, N)], K, 1, a, hip.GemvMode.kAdd, s.cuda_stream)
+        seq()
+        s.synchronize()
+        eager1 = host(y).copy()
+        seq()
+        s.synchronize()
+        eager2 = host(y).copy()
+        y.zero_()
+        s.synchronize()
+        g = hip.Graph(s)
+        with g:
+            seq()
+        for rep in range(3):
+            y.zero_()
+            s.synchronize()
+            g.launch()
+            s.synchronize()
+            assert np.array_equal(host(y), eager1), f"replay {rep}"
+            g.launch()
+            s.synchronize()
+            assert np.array_equal(host(y), eager2), f"double replay {rep}"
+            _ = (x * 2).sum().item()  # unrelated eager work between replays
+
+
+def test_invalid_arguments_raise(hip):
+    torch = _torch()
+    a = hip.Q8Act(zeros((1, 1024), torch.int8), zeros((1, 32), torch.float32), zeros((1, 32), torch.int32))
+    seg = hip.GemvSeg(zeros((4, 256), torch.uint8), zeros((4, 8), torch.int16), 4, zeros((1, 4), torch.float32), 4)
+    with pytest.raises(RuntimeError, match="multiple of 128"):
+        hip.launch_gemv([seg], 1000, 1, a, hip.GemvMode.kStore, stream())
+    with pytest.raises(RuntimeError, match="swiglu"):
+        hip.launch_gemv([seg], 1024, 1, a, hip.GemvMode.kSwiglu, stream())
+    with pytest.raises(RuntimeError, match="multiple of 32"):
+        hip.launch_prep(zeros((1, 1024), torch.float32), 1024, 1, 1000, None, 0.0, None, None, 0, a, stream())
