@@ -85,7 +85,7 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     r0 = (bid - wg0) * RB;
   }
 
-  // ---- activation registers for this lane's chunks ----
+  // ---- this lane's chunks ----
   int chunk[CL];
   bool cval[CL];
 #pragma unroll
@@ -93,6 +93,41 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     chunk[j] = (w * CL + j) * 16 + l16;
     cval[j] = chunk[j] < a.cpr;
   }
+  // ---- stream the rows ----
+  float acc[T][NB];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[t][b] = 0.f;
+  }
+
+  // Issue every code and scale load of the workgroup's rows first (the HBM
+  // stream), then the activation (L2-resident). The scheduling barriers keep
+  // the compiler from hoisting consumers of early loads above later issues,
+  // which would serialise the round trips.
+  u32x4 wv[T][CL];
+  uint32_t sc[T][CL];  // 32-bit: keeps every scale load in its own register
+  int rowv[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const int row = MODE == BTF_GEMV_SWIGLU ? r0 + 2 * t + (grp >> 1) : r0 + 4 * t + grp;
+    rowv[t] = row;
+    const int rowc = row < N ? row : N - 1;  // clamp: loads stay in bounds
+    const uint8_t* crow = cbase + (size_t)rowc * rowb;
+    const uint16_t* srow = sbase + (size_t)rowc * nsc;
+#pragma unroll
+    for (int j = 0; j < CL; ++j) {
+      // Unconditional (branch-free) loads: a lane past the row's last chunk
+      // reads chunk 0 again; its activation registers are zero, so it adds 0.
+      const int c = cval[j] ? chunk[j] : 0;
+      wv[t][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(crow + (size_t)c * 16));
+      sc[t][j] = __builtin_nontemporal_load(srow + (c >> 1));
+    }
+  }
+
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- activation registers ----
   uint32_t aq[NB][CL][16];
   float ad[NB][CL][2];
   int an[NB][CL][2];
@@ -126,42 +161,13 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     }
   }
 
-  // ---- stream the rows ----
-  float acc[T][NB];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[t][b] = 0.f;
-  }
-
-  // Issue every code and scale load of the workgroup's rows first.
-  u32x4 wv[T][CL];
-  uint16_t sc[T][CL];
-  int rowv[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const int row = MODE == BTF_GEMV_SWIGLU ? r0 + 2 * t + (grp >> 1) : r0 + 4 * t + grp;
-    rowv[t] = row;
-    const int rowc = row < N ? row : N - 1;  // clamp: loads stay in bounds
-    const uint8_t* crow = cbase + (size_t)rowc * rowb;
-    const uint16_t* srow = sbase + (size_t)rowc * nsc;
-#pragma unroll
-    for (int j = 0; j < CL; ++j) {
-      if (cval[j]) {
-        wv[t][j] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(crow + (size_t)chunk[j] * 16));
-        sc[t][j] = srow[chunk[j] >> 1];
-      } else {
-        wv[t][j] = u32x4{0u, 0u, 0u, 0u};
-        sc[t][j] = 0;
-      }
-    }
-  }
+  __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
     for (int j = 0; j < CL; ++j) {
-      const float f = h2f(sc[t][j]);
+      const float f = h2f((uint16_t)sc[t][j]);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int y0 = subblock_dot16(wv[t][j].x, wv[t][j].y, &aq[b][j][0], an[b][j][0]);
