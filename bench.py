@@ -3,22 +3,39 @@
 
 Default workload: the 27B-scale decode-step weight sweep at batch 1 --
 64 layers x (QKV 5120->7168, o 5120->5120 (+= residual), gate+up
-5120->17408 as one swiglu launch, down 17408->5120 (+= residual)) plus the
-untied output projection 5120->248,320, every GEMV preceded by the Q8
-quantize of its input, the whole step captured in one hipGraph.
-5,952,839,680 B of packed codes + scales per step, seeded synthetic weights
-(trits p = 0.3/0.4/0.3, fp16 scales U[0.01, 0.05]) and N(0,1) activations.
+5120->17408 as one swiglu GEMV, down 17408->5120 (+= residual)) plus the
+untied output projection 5120->248,320, every GEMV fed by the Q8 quantize of
+its input. 5,952,839,680 B of packed codes + scales per step, seeded
+synthetic weights (trits p = 0.3/0.4/0.3, fp16 scales U[0.01, 0.05]) and
+N(0,1) activations.
+
+Data flow of a layer (the same for both engines): QKV reads the residual
+stream, o adds W_o * (attention-output stand-in) into it, gate/up read the
+normed-input stand-in x, down adds W_down * h into it; the output
+projection reads the final residual. (Without the model's RMSNorm a residual
+feeding gate/up would grow quadratically and overflow; this keeps every
+value finite while still chaining every layer through the residual.)
+
+Engines:
+  step  (default at batch 1): the whole GEMV chain as ONE persistent launch
+        (btf_hip_step_*), each op's Q8 input produced by its producer;
+  graph: one hipGraph of quantize + GEMV launches (2 per GEMV), as the
+        reference decoder captures its step.
+The step engine's outputs are checked bit-exact against the graph engine's
+before timing ("verified" in the JSON line).
 
 `value` = algorithmic bytes of one step / measured step time (weights,
 activations and outputs already resident in HBM), in GB/s.
-`roofline` = the dominant GEMV kernel's algorithmic bytes per launch over its
-average launch time, measured with HIP events on its own stream.
+`roofline` = the dominant kernel's algorithmic bytes per launch over its
+average launch time from HIP events on the stream it runs on (the step
+engine: the step kernel itself, one launch per step).
 `cpu_baseline` = the reference's CPU emulator GEMV (oracle/_ref, built from
 the reference sources) or the oracle port, timed on this host on a bounded
-sample of the same workload.
+sample of the same workload (about --cpu-budget seconds).
 
-Other workloads (--workload layer|batched|prefill) report configs 2-4 the
-same way; they are measurement aids, the default line is the sweep.
+Other workloads (--workload layer|batched|prefill) report the other
+configurations the same way; they are measurement aids, the default line is
+the sweep.
 """
 from __future__ import annotations
 
@@ -114,7 +131,8 @@ class Step:
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
         self.x = dev(rng.standard_normal((M, E)).astype(np.float32))     # normed hidden state stand-in
         self.xo = dev(rng.standard_normal((M, E)).astype(np.float32))    # attention-output stand-in
-        self.res = torch.zeros((M, E), dtype=torch.float32, device="cuda")
+        self.res0 = rng.standard_normal((M, E)).astype(np.float32)       # residual stream at step start
+        self.res = dev(self.res0)
         self.qkv = torch.zeros((M, QKV), dtype=torch.float32, device="cuda")
         self.h = torch.zeros((M, F), dtype=torch.float32, device="cuda")
         self.logits = torch.zeros((1, V), dtype=torch.float32, device="cuda") if with_output else None
@@ -146,7 +164,7 @@ class Step:
 
     def layer(self, l, st):
         S, M, G = self.S, self.M, self.S.hip.GemvMode
-        self.prep(self.x, E, M, st)
+        self.prep(self.res, E, M, st)
         self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
         self.prep(self.xo, E, M, st)
         self.gemv([S.seg("o", l, self.res, E)], E, M, G.kAdd, st)
@@ -159,8 +177,38 @@ class Step:
         for l in range(self.layers):
             self.layer(l, st)
         if self.with_output:
-            self.prep(self.x, E, 1, st)
+            self.prep(self.res, E, 1, st)
             self.gemv([self.S.seg("output", self.layers, self.logits, V)], E, 1, self.S.hip.GemvMode.kStore, st)
+
+    def reset(self):
+        self.res.copy_(self.S.torch.from_numpy(self.res0).cuda())
+
+    def program(self):
+        """The same chain as one step program (batch 1). Vector slots:
+        0 residual, 1 qkv, 2 attention-output stand-in, 3 x, 4 h, 5 logits."""
+        hip, S, G = self.S.hip, self.S, self.S.hip.GemvMode
+        assert self.M == 1
+        vecs = [hip.StepVec(E, self.res), hip.StepVec(QKV, self.qkv), hip.StepVec(E, self.xo),
+                hip.StepVec(E, self.x), hip.StepVec(F, self.h)]
+        if self.with_output:
+            vecs.append(hip.StepVec(V, self.logits))
+        base = S.arena.data_ptr()
+
+        def w(name, l):
+            N, K, _, co, so = S.mats[(name, l)]
+            return base + co, base + so
+
+        ops = []
+        for l in range(self.layers):
+            ops.append(hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1))
+            ops.append(hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0))
+            gc, gs = w("gate", l)
+            uc, us = w("up", l)
+            ops.append(hip.StepGemv(G.kSwiglu, E, F, gc, gs, 3, 4, uc, us))
+            ops.append(hip.StepGemv(G.kAdd, F, E, *w("down", l), 4, 0))
+        if self.with_output:
+            ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 5))
+        return hip.StepProgram(vecs, ops)
 
     def kind_launch(self, kind, l, st):
         """One GEMV launch of a given kind (for per-kernel timing)."""
@@ -200,6 +248,45 @@ def time_graph(hip, torch, fn, reps, warmup):
     return ms, g
 
 
+def time_program(hip, torch, prog, reps, warmup):
+    """warmup + reps launches of a step program on one stream; ms per launch
+    from HIP events recorded on that stream."""
+    s = torch.cuda.Stream()
+    for _ in range(warmup):
+        prog.launch(s.cuda_stream)
+    s.synchronize()
+    e0, e1 = hip.Event(), hip.Event()
+    e0.record(s)
+    for _ in range(reps):
+        prog.launch(s.cuda_stream)
+    e1.record(s)
+    s.synchronize()
+    if prog.error():
+        raise RuntimeError("step program reported a timeout")
+    return e0.elapsed_ms(e1) / reps
+
+
+def verify_step_vs_graph(torch, step: Step, prog):
+    """Bit-exact comparison of one step-program launch with the op-by-op
+    launches of the same chain from the same residual."""
+    import numpy as np
+    outs = []
+    for run in (lambda st: step.run(st), lambda st: prog.launch(st)):
+        step.reset()
+        torch.cuda.synchronize()
+        run(torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append([t.cpu().numpy().copy() for t in (step.res, step.qkv, step.h, step.logits) if t is not None])
+    if prog.error():
+        return False, "step program reported a timeout"
+    for a, b in zip(*outs):
+        if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
+            return False, f"max |diff| {float(np.max(np.abs(a - b))):.3e}"
+    if not all(np.isfinite(a).all() for a in outs[0]):
+        return False, "non-finite outputs"
+    return True, "bit-exact"
+
+
 def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
     """The reference CPU emulator's GEMV (or the oracle port) on a bounded sample
     of the same workload: the projections of the first layers, M rows."""
@@ -230,11 +317,15 @@ def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
                     break
     except OSError:
         pass
+    # Host copies of up to 8 layers (about 750 MB, well beyond the host's
+    # caches), cycled until the time budget is spent.
+    nl = min(step.layers, 8)
+    names = (("qkv", E), ("o", E), ("gate", E), ("up", E), ("down", F))
+    host = {(name, l): S.host_mat(name, l) for l in range(nl) for name, _ in names}
     l = 0
-    while total_t < budget_s and l < min(step.layers, 8):
-        mats = [(name, K) for name, K in (("qkv", E), ("o", E), ("gate", E), ("up", E), ("down", F))]
-        for name, K in mats:
-            codes, scales = S.host_mat(name, l)
+    while total_t < budget_s:
+        for name, K in names:
+            codes, scales = host[(name, l % nl)]
             q, d, s_ = (qe, de, se) if K == E else (qf, df, sf)
             t0 = time.perf_counter()
             O.quantize_rows(xe if K == E else xf)  # the Q8 quantize of the input
@@ -253,7 +344,8 @@ def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
     gbs = total_b / total_t / 1e9
     return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
             "tok_s_equiv": round(total_b / total_t / step.total_bytes, 4) if M == 1 else None,
-            "sample": f"{layers_done} layer(s) x (QKV 5120->7168, o 5120->5120, gate/up 5120->17408, "
+            "sample": f"{layers_done} layer GEMV set(s), cycling over {nl} distinct layers, "
+                      f"x (QKV 5120->7168, o 5120->5120, gate/up 5120->17408, "
                       f"down 17408->5120), M={M}, each GEMV with its Q8 quantize; "
                       f"{'reference EmuDecoder::gemv (src/emu_decoder.cpp:143-165) built from the reference sources' if kind == 'reference' else 'oracle port of EmuDecoder::gemv'}, "
                       f"{total_t:.2f} s of CPU time; host CPU: {cpu_model}"}
@@ -269,6 +361,10 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--engine", default="auto", choices=["auto", "step", "graph"],
+                    help="auto: at batch 1 both engines are timed and the faster one is the value; "
+                         "the graph otherwise")
+    ap.add_argument("--no-kinds", action="store_true", help="skip the per-GEMV-kind graph timings")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -300,38 +396,69 @@ def main():
     else:
         step = Step(S, 512, layers, with_output=False)
 
-    ms, g = time_graph(hip, torch, step.run, args.steps, args.warmup)
-    log(f"step: {ms:.4f} ms ({step.total_bytes / 1e9:.4f} GB algorithmic)")
+    engines = [args.engine] if args.engine != "auto" else (["step", "graph"] if step.M == 1 else ["graph"])
+    if "step" in engines and step.M != 1:
+        raise SystemExit("the step engine runs batch-1 chains only")
+
+    verified = None
+    engine_ms = {}
+    if "step" in engines:
+        t0 = time.time()
+        prog = step.program()
+        log(f"step program built in {time.time() - t0:.2f} s")
+        ok, why = verify_step_vs_graph(torch, step, prog)
+        verified = {"vs_graph_engine": ok, "detail": why}
+        log(f"step program vs op-by-op launches: {why}")
+        if not ok:
+            raise SystemExit(f"step program does not match the op-by-op launches: {why}")
+        step.reset()
+        engine_ms["step"] = time_program(hip, torch, prog, args.steps, args.warmup)
+        log(f"step engine: {engine_ms['step']:.4f} ms per step")
+    if "graph" in engines:
+        step.reset()
+        engine_ms["graph"], g = time_graph(hip, torch, step.run, args.steps, args.warmup)
+        log(f"graph engine: {engine_ms['graph']:.4f} ms per step")
+    engine = min(engine_ms, key=engine_ms.get)
+    ms = engine_ms[engine]
+    kernels_per_step = 1 if engine == "step" else layers * 8 + (2 if step.with_output else 0)
+    log(f"{engine} engine reported: {ms:.4f} ms per step ({step.total_bytes / 1e9:.4f} GB algorithmic)")
     value = step.total_bytes / (ms / 1e3) / 1e9
 
-    # Per-kind GEMV timing: a graph of one launch per layer (distinct weights,
-    # > 256 MB working set except for a single layer) -> average per launch.
+    # Per-kind GEMV timing of the op-by-op path: a graph of one launch per
+    # layer (distinct weights) -> average per launch.
     kinds = ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else [])
     per = {}
-    for kind in kinds:
-        reps = 1 if kind == "output" else layers
-        fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st)) if kind == "output" else \
-             (lambda st, kind=kind: [step.kind_launch(kind, l, st) for l in range(layers)])
-        kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
-        avg_us = kms * 1e3 / reps
-        b = step.kind_bytes[kind] if kind != "output" else step.kind_bytes["output"]
-        per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
-                     "launches_per_step": 1 if kind == "output" else layers}
-        log(f"  {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
-    dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
-    d = per[dom]
-    if step.M <= 32:
-        roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'})",
-                "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
+    if not args.no_kinds or engine == "graph":
+        for kind in kinds:
+            reps = 1 if kind == "output" else layers
+            fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st)) if kind == "output" else \
+                 (lambda st, kind=kind: [step.kind_launch(kind, l, st) for l in range(layers)])
+            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            avg_us = kms * 1e3 / reps
+            b = step.kind_bytes[kind]
+            per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
+                         "launches_per_step": 1 if kind == "output" else layers}
+            log(f"  op-by-op {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
+    if engine == "step":
+        roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "step_kernel (the whole GEMV chain, one launch per step)",
+                "bytes_per_launch": step.total_bytes, "avg_launch_us": round(ms * 1e3, 3)}
     else:
-        K_ = F if dom == "down" else E
-        N_ = {"qkv": QKV, "o": E, "gateup": 2 * F, "down": E}[dom]
-        tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
-        roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                "kernel": f"{dom} GEMM (gemm_mfma_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
+        dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
+        d = per[dom]
+        if step.M <= 32:
+            roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                    "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'})",
+                    "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
+        else:
+            K_ = F if dom == "down" else E
+            N_ = {"qkv": QKV, "o": E, "gateup": 2 * F, "down": E}[dom]
+            tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
+            roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                    "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                    "kernel": f"{dom} GEMM (gemm_mfma_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
 
     out = {
         "metric": METRIC,
@@ -349,19 +476,22 @@ def main():
         "config": {
             "workload": {"sweep": f"27B-scale decode-step weight sweep: {layers} x (QKV 5120->7168, o 5120->5120, "
                                   "gate+up 5120->17408 swiglu, down 17408->5120) + output 5120->248320, "
-                                  "batch 1, Q8 quantize before every GEMV, one hipGraph",
+                                  "batch 1, every GEMV fed by the Q8 quantize of its input",
                          "layer": "one decoder layer's projections at batch 1, each with its Q8 quantize",
                          "batched": f"batched decode, M={step.M}, {layers} layers of the 27B shapes",
                          "prefill": f"prefill M=512, {layers} layers of the 27B shapes"}[args.workload],
             "batch": step.M,
             "bytes_per_step": step.total_bytes,
             "weight_bytes_per_step": step.weight_bytes,
-            "kernels_per_step": layers * 8 + (2 if step.with_output else 0),
+            "engine": engine,
+            "kernels_per_step": kernels_per_step,
             "parallelism": "single GPU",
         },
         "frac_of_8TBs": round(value / HBM_PEAK_GBS, 4),
         "tok_s_equiv": round(1e3 / ms, 2) if args.workload == "sweep" else None,
         "roofline": roof,
+        "verified": verified,
+        "engines_ms": {k: round(v, 4) for k, v in engine_ms.items()},
         "gemv_kinds": per,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},
     }

@@ -44,6 +44,15 @@ class _GemvSeg(C.Structure):
                 ("ldy", C.c_int)]
 
 
+class _StepVec(C.Structure):
+    _fields_ = [("n", C.c_int), ("data", C.c_void_p)]
+
+
+class _StepGemv(C.Structure):
+    _fields_ = [("mode", C.c_int), ("K", C.c_int), ("N", C.c_int), ("codes", C.c_void_p), ("scales", C.c_void_p),
+                ("up_codes", C.c_void_p), ("up_scales", C.c_void_p), ("in_vec", C.c_int), ("out_vec", C.c_int)]
+
+
 class _DeviceInfo(C.Structure):
     _fields_ = [("cu_count", C.c_int), ("lds_bytes_per_block", C.c_int), ("max_clock_khz", C.c_int),
                 ("mem_clock_khz", C.c_int), ("mem_bus_width_bits", C.c_int), ("l2_bytes", C.c_int),
@@ -80,6 +89,12 @@ _event_record = _decl("btf_hip_event_record", [_vp, _vp])
 _event_elapsed = _decl("btf_hip_event_elapsed_ms", [C.POINTER(C.c_float), _vp, _vp])
 _host_alloc_mapped = _decl("btf_hip_host_alloc_mapped", [C.POINTER(C.c_void_p), C.POINTER(C.c_void_p), C.c_size_t])
 _host_free = _decl("btf_hip_host_free", [_vp])
+_step_create = _decl("btf_hip_step_create",
+                     [C.POINTER(_StepVec), _i, C.POINTER(_StepGemv), _i, C.POINTER(C.c_void_p)])
+_step_launch = _decl("btf_hip_step_launch", [_vp, _vp])
+_step_error = _decl("btf_hip_step_error", [_vp, C.POINTER(C.c_int)])
+_step_destroy = _decl("btf_hip_step_destroy", [_vp])
+_step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
 
 #: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
 ABI_SYMBOLS = (
@@ -90,7 +105,8 @@ ABI_SYMBOLS = (
     "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
     "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
     "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
-    "btf_hip_graph_destroy",
+    "btf_hip_graph_destroy", "btf_hip_step_create", "btf_hip_step_launch", "btf_hip_step_error",
+    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit",
 )
 
 
@@ -224,6 +240,80 @@ def gen_ptq1_0(seed: int, mat: int, first_block: int, nblocks: int, dst, stream=
     _check(_gen(seed, mat, first_block, nblocks, _addr(dst), _stream(stream)))
 
 
+@dataclass
+class StepVec:
+    """A vector slot of a step program: length n and optional device fp32 data."""
+    n: int
+    data: object = None
+
+
+@dataclass
+class StepGemv:
+    """One GEMV of a step program (swiglu: codes/scales = gate, up_* = up)."""
+    mode: int
+    K: int
+    N: int
+    codes: object
+    scales: object
+    in_vec: int
+    out_vec: int
+    up_codes: object = None
+    up_scales: object = None
+
+
+class StepProgram:
+    """A decode step's GEMV chain run as one persistent launch
+    (btf_hip_step_create / _launch / _error / _destroy). The vectors' data
+    tensors must stay alive while the program exists."""
+
+    def __init__(self, vecs, gemvs):
+        cv = (_StepVec * len(vecs))(*[_StepVec(v.n, _addr(v.data)) for v in vecs])
+        cg = (_StepGemv * len(gemvs))(*[
+            _StepGemv(int(g.mode), g.K, g.N, _addr(g.codes), _addr(g.scales), _addr(g.up_codes), _addr(g.up_scales),
+                      g.in_vec, g.out_vec) for g in gemvs])
+        h = C.c_void_p()
+        _check(_step_create(cv, len(vecs), cg, len(gemvs), C.byref(h)))
+        self.h = h.value
+        self._keep = (vecs, gemvs)
+
+    def launch(self, stream=None):
+        _check(_step_launch(self.h, _stream(stream)))
+
+    def launch_raw(self, stream=None) -> int:
+        return _step_launch(self.h, _stream(stream))
+
+    def error(self) -> int:
+        """Device error flag of the launches since the last call (1 = a launch
+        timed out waiting for data); clears it. Synchronise first."""
+        e = C.c_int()
+        _check(_step_error(self.h, C.byref(e)))
+        return e.value
+
+    def set_spin_limit(self, polls: int):
+        _check(_step_spin(self.h, polls))
+
+    def close(self, _destroy=_step_destroy):
+        if getattr(self, "h", None):
+            _destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+def step_create_raw(vecs, gemvs) -> int:
+    """Status code of btf_hip_step_create (the program is destroyed at once)."""
+    cv = (_StepVec * max(1, len(vecs)))(*[_StepVec(v.n, _addr(v.data)) for v in vecs])
+    cg = (_StepGemv * max(1, len(gemvs)))(*[
+        _StepGemv(int(g.mode), g.K, g.N, _addr(g.codes), _addr(g.scales), _addr(g.up_codes), _addr(g.up_scales),
+                  g.in_vec, g.out_vec) for g in gemvs])
+    h = C.c_void_p()
+    rc = _step_create(cv, len(vecs), cg, len(gemvs), C.byref(h))
+    if rc == BTF_OK:
+        _step_destroy(h.value)
+    return rc
+
+
 def last_error() -> str:
     return _last_error().decode()
 
@@ -256,9 +346,9 @@ class Graph:
     def launch(self):
         _check(_graph_launch(self.exec, self.stream))
 
-    def __del__(self):
+    def __del__(self, _destroy=_graph_destroy):
         if self.exec:
-            _graph_destroy(self.exec)
+            _destroy(self.exec)
             self.exec = None
 
 
@@ -278,9 +368,9 @@ class Event:
         _check(_event_elapsed(C.byref(ms), self.h, end.h))
         return ms.value
 
-    def __del__(self):
+    def __del__(self, _destroy=_event_destroy):
         if getattr(self, "h", None):
-            _event_destroy(self.h)
+            _destroy(self.h)
             self.h = None
 
 
@@ -296,9 +386,9 @@ class MappedHostBuffer:
         import numpy as np
         return np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.host))
 
-    def close(self):
+    def close(self, _free=_host_free):
         if self.host:
-            _host_free(self.host)
+            _free(self.host)
             self.host = None
 
     def __del__(self):

@@ -213,6 +213,37 @@ int btf_hip_gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t
   return gen_ptq1_0(seed, mat, first_block, nblocks, dst, static_cast<hipStream_t>(stream), *ds);
 }
 
+int btf_hip_step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops, btf_step_t* out) {
+  if (!vecs || !ops || !out || nvec <= 0 || nops <= 0) return fail(BTF_ERR_ARGS, "step: empty program");
+  if (const int rc = step_validate(vecs, nvec, ops, nops)) return rc;
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  StepProgram* P = nullptr;
+  const int rc = step_create(vecs, nvec, ops, nops, &P, *ds);
+  if (rc == BTF_OK) *out = P;
+  return rc;
+}
+
+int btf_hip_step_launch(btf_step_t prog, btf_stream_t stream) {
+  if (!prog) return fail(BTF_ERR_ARGS, "step: null program");
+  return step_launch(static_cast<StepProgram*>(prog), static_cast<hipStream_t>(stream));
+}
+
+int btf_hip_step_error(btf_step_t prog, int* error) {
+  if (!prog || !error) return fail(BTF_ERR_ARGS, "step: null argument");
+  return step_error(static_cast<StepProgram*>(prog), error);
+}
+
+int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls) {
+  if (!prog) return fail(BTF_ERR_ARGS, "step: null program");
+  return step_set_spin_limit(static_cast<StepProgram*>(prog), polls);
+}
+
+int btf_hip_step_destroy(btf_step_t prog) {
+  step_destroy(static_cast<StepProgram*>(prog));
+  return BTF_OK;
+}
+
 const char* btf_hip_last_error(void) { return g_err.c_str(); }
 
 int btf_hip_device_info(int device, btf_device_info* out) {

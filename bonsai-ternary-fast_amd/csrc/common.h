@@ -6,6 +6,8 @@
 #include <cstdint>
 #include <string>
 
+#include "../../include/btf/hip_abi.h"
+
 namespace btfhip {
 
 // ---- T2 / Q8 geometry (the reference's include/btf/packed.hpp:29-32) ----
@@ -33,14 +35,17 @@ int launch_status(const char* what);  // hipGetLastError -> BTF_ERR_LAUNCH
 
 // ---- wave64 reductions with DPP (no LDS) ----
 // dpp_ctrl encodings (GCN3+/CDNA): quad_perm(a,b,c,d) = a | b<<2 | c<<4 | d<<6,
-// row_half_mirror = 0x141, row_mirror = 0x140.
+// row_half_mirror = 0x141, row_mirror = 0x140. Every pattern used here is a
+// permutation within each 16-lane row with all rows and banks enabled, so no
+// lane reads an invalid source; bound_ctrl lets the compiler fuse the move
+// into the consuming add (v_add_f32_dpp).
 template <int CTRL>
 __device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
 template <int CTRL>
 __device__ __forceinline__ int dpp_i(int v) {
-  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, true);
 }
 // Sum over each 16-lane DPP row; every lane of the row gets the total.
 // Butterfly: swap neighbours, swap pairs, mirror halves of 8, mirror halves of 16.
@@ -126,6 +131,16 @@ int repack(const uint8_t* src, int64_t nblocks, uint8_t* codes, uint16_t* scales
 int prep(const float* x, int ldx, int M, int n, const float* normw, float eps, int block, int perm_hd, int perm_nk,
          int perm_rep, const float* signs, float* xn_out, int ldxn, int8_t* q, float* d, int32_t* s, hipStream_t st,
          const DevState& ds);
+struct StepProgram;
+int step_validate(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops);  // host only
+int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops, StepProgram** out,
+                const DevState& ds);
+int step_check_residency(const DevState& ds);
+int step_launch(StepProgram* P, hipStream_t st);
+int step_error(StepProgram* P, int* err);
+int step_set_spin_limit(StepProgram* P, uint32_t polls);
+void step_destroy(StepProgram* P);
+
 int gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst, hipStream_t st,
                const DevState& ds);
 

@@ -14,9 +14,12 @@
 //    d/16 and -s of its 2 sub-blocks) is loaded once into registers and
 //    reused for all T row steps.
 //  * The 4 groups of a wave (l >> 4) take 4 different rows per step.
-//  * Per row: lane partial -> 16-lane DPP butterfly -> LDS [wave][row] ->
-//    fixed-order sum over waves -> epilogue. The float order is fixed, so
-//    results are deterministic run to run.
+//  * Per row and 1024-column slice (16 lanes x 64 columns): lane partial ->
+//    16-lane DPP butterfly -> LDS [slice][row] -> fixed-order sum over the
+//    slices -> epilogue. The float order is fixed (deterministic run to run)
+//    and does not depend on how slices are spread over waves, so the
+//    persistent step kernel, which walks the same slices, gives identical
+//    results.
 #include <climits>
 
 #include "../../include/btf/hip_abi.h"
@@ -49,7 +52,7 @@ constexpr int kMaxWaves = 16;
 template <int CL, int NB, int T, int MODE, bool DUMP>
 __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
   constexpr int RB = 4 * T;  // virtual rows per workgroup (4 per step)
-  __shared__ float red[NB][kMaxWaves][RB];
+  __shared__ float red[NB][kMaxWaves * CL][RB];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -94,12 +97,7 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     cval[j] = chunk[j] < a.cpr;
   }
   // ---- stream the rows ----
-  float acc[T][NB];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-#pragma unroll
-    for (int b = 0; b < NB; ++b) acc[t][b] = 0.f;
-  }
+  float acc[T][NB][CL];  // one partial per 1024-column slice
 
   // Issue every code and scale load of the workgroup's rows first (the HBM
   // stream), then the activation (L2-resident). The scheduling barriers keep
@@ -181,23 +179,27 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
         } else {
           float p = ad[b][j][0] * (float)y0;
           p = fmaf(ad[b][j][1], (float)y1, p);
-          acc[t][b] = fmaf(f, p, acc[t][b]);
+          acc[t][b][j] = f * p;
         }
       }
     }
   }
   if constexpr (DUMP) return;
 
-  // ---- reduce: 16 lanes -> one value per (row, activation row) and wave ----
+  // ---- reduce: 16 lanes -> one value per (row, activation row) and slice ----
 #pragma unroll
   for (int t = 0; t < T; ++t) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const float v = row16_sum(acc[t][b]);
-      if (l16 == 0) red[b][w][4 * t + grp] = v;
+#pragma unroll
+      for (int j = 0; j < CL; ++j) {
+        const float v = row16_sum(acc[t][b][j]);
+        if (l16 == 0) red[b][w * CL + j][4 * t + grp] = v;
+      }
     }
   }
   __syncthreads();
+  const int nsl = nw * CL;  // slices; those past the row end hold +0
 
   // ---- epilogue: fixed-order sum over waves ----
   for (int i = threadIdx.x; i < NB * RB; i += blockDim.x) {
@@ -208,15 +210,15 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     if constexpr (MODE == BTF_GEMV_SWIGLU) {
       if (v & 1) continue;
       float g = 0.f, u = 0.f;
-      for (int ww = 0; ww < nw; ++ww) {
-        g += red[b][ww][v];
-        u += red[b][ww][v + 1];
+      for (int k = 0; k < nsl; ++k) {
+        g += red[b][k][v];
+        u += red[b][k][v + 1];
       }
       const int row = r0 + (v >> 1);
       if (row < N) y[m * ldy + row] = g / (1.0f + expf(-g)) * u;
     } else {
       float sum = 0.f;
-      for (int ww = 0; ww < nw; ++ww) sum += red[b][ww][v];
+      for (int k = 0; k < nsl; ++k) sum += red[b][k][v];
       const int row = r0 + v;
       if (row < N) {
         if constexpr (MODE == BTF_GEMV_ADD)
@@ -244,7 +246,7 @@ void by_mode(int mode, const Dot4Args& a, int grid, int threads, hipStream_t st)
 }
 
 // Instantiated shapes: CL=1 with NB 1/2 (T 2/4/8) and NB 4 (T 2); CL=2 with
-// NB 1 (T 2/4/8). Every one of them fits 128 VGPRs without scratch.
+// NB 1 (T 2/4). Every one of them fits 128 VGPRs without scratch.
 template <int CL, int NB>
 void by_t(int T, int mode, bool dump, const Dot4Args& a, int grid, int threads, hipStream_t st) {
   if (dump) {
@@ -253,6 +255,11 @@ void by_t(int T, int mode, bool dump, const Dot4Args& a, int grid, int threads, 
   }
   if constexpr (CL * NB >= 4) {
     by_mode<CL, NB, 2, false>(mode, a, grid, threads, st);
+  } else if constexpr (CL == 2) {
+    if (T == 2)
+      by_mode<CL, NB, 2, false>(mode, a, grid, threads, st);
+    else
+      by_mode<CL, NB, 4, false>(mode, a, grid, threads, st);
   } else {
     switch (T) {
       case 2: by_mode<CL, NB, 2, false>(mode, a, grid, threads, st); break;
@@ -281,6 +288,7 @@ int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   int T = 8;
   while (T > 2 && rows / (unit * T) < 2L * ds.cu_count) T /= 2;
   if (NB * CL >= 4 && T > 2) T = 2;  // register budget
+  if (CL == 2 && T > 4) T = 4;
   if (dump) T = 2;
 
   Dot4Args a{};

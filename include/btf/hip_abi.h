@@ -122,6 +122,48 @@ int btf_hip_gemv_set_policy(int mfma_min_m);
 int btf_hip_gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst,
                        btf_stream_t stream);
 
+/* ---- decode-step program: a chain of GEMVs in one launch ----------------
+ * No counterpart in the reference's launch API: it replaces the reference
+ * decoder's per-step graph of launches (src/cuda/gpu_decoder.cu:452-486) for
+ * the GEMV chain. A program has vector slots and GEMV ops in order; each op
+ * reads the first K values of its input vector, quantizes them (Q8_0, as
+ * launch_prep without norm or transform) and writes its output vector
+ * (STORE: y = W q; ADD: y += W q; SWIGLU: y = silu(W_g q) * (W_u q)), all
+ * with the same arithmetic as btf_hip_launch_gemv. Vectors read before any
+ * op writes them take their values from `data` at launch; the final value of
+ * a vector (the result of the last op that writes it) is written to its
+ * `data` when that is non-NULL. Vectors must not overlap in memory.
+ * Creation allocates the program's device buffers and needs every workgroup
+ * of the launch co-resident (one per CU); launches allocate nothing. One
+ * launch at a time per program (launches on one stream serialise). */
+typedef struct btf_step_vec {
+  int n;       /* length (multiple of 32 when it is quantized) */
+  float* data; /* device fp32 [n], or NULL for a vector internal to the step */
+} btf_step_vec;
+typedef struct btf_step_gemv {
+  int mode; /* BTF_GEMV_STORE / ADD / SWIGLU */
+  int K;    /* input width, multiple of 128, <= 20480 */
+  int N;    /* output rows == length of the output vector */
+  const uint8_t* codes;      /* [N][K/4]   (swiglu: gate) */
+  const uint16_t* scales;    /* [N][K/128] */
+  const uint8_t* up_codes;   /* swiglu: up matrix, else NULL */
+  const uint16_t* up_scales;
+  int in_vec, out_vec; /* vector slot indices (must differ) */
+} btf_step_gemv;
+typedef void* btf_step_t;
+int btf_hip_step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops, btf_step_t* out);
+/* One cooperative launch running every op of the program. */
+int btf_hip_step_launch(btf_step_t prog, btf_stream_t stream);
+/* Synchronous read of the program's device error flag (0 = ok; 1 = a launch
+ * timed out waiting for data, its outputs are invalid), then clears it. Call
+ * after the launch's stream has been synchronised. */
+int btf_hip_step_error(btf_step_t prog, int* error);
+int btf_hip_step_destroy(btf_step_t prog);
+/* Test hook: bound on the number of polls of every wait in the program's
+ * later launches (0 restores the default, about one second). A tiny bound
+ * makes a launch give up waiting and set the error flag instead of hanging. */
+int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls);
+
 /* Device description for reports. name must hold name_len bytes. */
 typedef struct btf_device_info {
   int cu_count;

@@ -1,0 +1,106 @@
+// kernels.hpp -- C++ mirror of the reference's kernel-launch API for the
+// fused ternary matmul path (src/cuda/kernels.cuh:13-56, namespace
+// btf::cuda), implemented over the C ABI of libbtf_hip.so (hip_abi.h).
+//
+// Same names, struct fields, defaults and argument meaning as the reference;
+// the namespace is btf::hip and the stream is a hipStream_t (any pointer-
+// sized stream handle converts to btf_stream_t). Failures throw
+// std::runtime_error with the library's message, as the reference launchers
+// do. Header-only; link with -lbtf_hip.
+#pragma once
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+#include "hip_abi.h"
+
+namespace btf {
+namespace hip {
+
+namespace detail {
+inline void check(int rc, const char* what) {
+  if (rc != BTF_OK) {
+    const char* msg = btf_hip_last_error();
+    throw std::runtime_error(std::string(what) + ": " + (msg && *msg ? msg : "error " + std::to_string(rc)));
+  }
+}
+}  // namespace detail
+
+// kernels.cuh:17 -- once per device before any launch or capture.
+inline void kernels_init(int device) { detail::check(btf_hip_kernels_init(device), "kernels_init"); }
+
+// kernels.cuh:20
+inline int gemv_max_nb(int K) { return btf_hip_gemv_max_nb(K); }
+
+// kernels.cuh:22-24
+inline void launch_repack(const uint8_t* src, int64_t nblocks, uint8_t* codes, uint16_t* scales,
+                          btf_stream_t st) {
+  detail::check(btf_hip_launch_repack(src, nblocks, codes, scales, st), "launch_repack");
+}
+
+// kernels.cuh:26-31
+struct Q8Act {
+  int8_t* q = nullptr;  // [M][K]
+  float* d = nullptr;   // [M][K/32]
+  int* s = nullptr;     // [M][K/32] sum of q per block
+};
+
+// kernels.cuh:33-38
+struct Hx {
+  int block = 0;
+  int perm_hd = 0, perm_nk = 0, perm_rep = 0;
+  const float* signs = nullptr;
+};
+
+// kernels.cuh:40-43
+inline void launch_prep(const float* x, int ldx, int M, int n, const float* normw, float eps, const Hx& hx,
+                        float* xn_out, int ldxn, const Q8Act& a, btf_stream_t st) {
+  const btf_hx h{hx.block, hx.perm_hd, hx.perm_nk, hx.perm_rep, hx.signs};
+  const btf_q8act q{a.q, a.d, reinterpret_cast<int32_t*>(a.s)};
+  detail::check(btf_hip_launch_prep(x, ldx, M, n, normw, eps, &h, xn_out, ldxn, &q, st), "launch_prep");
+}
+
+// kernels.cuh:45-52
+struct GemvSeg {
+  const uint8_t* codes = nullptr;
+  const uint16_t* scales = nullptr;
+  int N = 0;
+  float* y = nullptr;
+  int ldy = 0;
+};
+enum GemvMode { kStore = BTF_GEMV_STORE, kAdd = BTF_GEMV_ADD, kSwiglu = BTF_GEMV_SWIGLU };
+
+// kernels.cuh:53-56
+inline void launch_gemv(const GemvSeg* segs, int nseg, int K, int M, const Q8Act& a, GemvMode mode,
+                        btf_stream_t st) {
+  if (nseg < 1 || nseg > 3) throw std::runtime_error("launch_gemv: gemv: 1..3 segments");
+  btf_gemv_seg s[3] = {};
+  for (int i = 0; i < nseg; ++i) s[i] = btf_gemv_seg{segs[i].codes, segs[i].scales, segs[i].N, segs[i].y, segs[i].ldy};
+  const btf_q8act q{a.q, a.d, reinterpret_cast<int32_t*>(a.s)};
+  detail::check(btf_hip_launch_gemv(s, nseg, K, M, &q, mode, st), "launch_gemv");
+}
+
+// ---- the decode-step program (no counterpart in kernels.cuh: it replaces
+// the per-step graph of GEMV launches, src/cuda/gpu_decoder.cu:452-486)
+class StepProgram {
+ public:
+  StepProgram(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops) {
+    detail::check(btf_hip_step_create(vecs, nvec, ops, nops, &p_), "step_create");
+  }
+  StepProgram(const StepProgram&) = delete;
+  StepProgram& operator=(const StepProgram&) = delete;
+  ~StepProgram() { (void)btf_hip_step_destroy(p_); }
+  void launch(btf_stream_t st) { detail::check(btf_hip_step_launch(p_, st), "step_launch"); }
+  // true if a launch since the last call timed out (synchronise first); clears it
+  bool failed() {
+    int e = 0;
+    detail::check(btf_hip_step_error(p_, &e), "step_error");
+    return e != 0;
+  }
+
+ private:
+  btf_step_t p_ = nullptr;
+};
+
+}  // namespace hip
+}  // namespace btf

@@ -8,16 +8,17 @@ tests do not depend on the GPU quantizer.
 import numpy as np
 
 
-def random_ptq(oracle, rng, N, K):
-    """PTQ1_0 bytes [N][K/128*28] like the reference's random_ptq."""
-    w = rng.standard_normal((N, K)).astype(np.float32)
+def random_ptq(oracle, rng, N, K, scale=1.0):
+    """PTQ1_0 bytes [N][K/128*28] like the reference's random_ptq (times
+    `scale`, which sets the magnitude of the fp16 block scales)."""
+    w = rng.standard_normal((N, K)).astype(np.float32) * np.float32(scale)
     w *= (rng.random((N, K)) >= 0.3).astype(np.float32)
     return oracle.quant_ptq1_0(w)
 
 
-def random_mat(oracle, rng, N, K):
+def random_mat(oracle, rng, N, K, scale=1.0):
     """(codes [N][K/4], scales [N][K/128]) of a random PTQ1_0 matrix."""
-    src = random_ptq(oracle, rng, N, K)
+    src = random_ptq(oracle, rng, N, K, scale)
     return oracle.repack_rows(src, N, K)
 
 

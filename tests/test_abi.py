@@ -1,0 +1,153 @@
+"""CPU tests of the C ABI boundary (include/btf/hip_abi.h, libbtf_hip.so):
+the library loads without a GPU, exports exactly what the header declares,
+rejects invalid arguments on the host before any HIP call (as the reference
+launchers validate before launching, src/cuda/kernels.cu:737-822), and the
+C header / C++ mirror (include/btf/kernels.hpp) compile and link as a
+reference-side caller would use them.
+"""
+import ctypes as C
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include")
+PKG = os.path.join(ROOT, "bonsai-ternary-fast_amd")
+LIB = os.path.join(PKG, "libbtf_hip.so")
+
+pytestmark = pytest.mark.skipif(not os.path.exists(LIB), reason="libbtf_hip.so not built")
+
+
+def header_symbols():
+    text = open(os.path.join(INC, "btf", "hip_abi.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(btf_hip_\w+)\s*\(", text)))
+
+
+def test_header_symbols_exported():
+    lib = C.CDLL(LIB)
+    syms = header_symbols()
+    assert len(syms) >= 30
+    missing = [s for s in syms if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_python_mirror_lists_every_symbol():
+    import btf_hip
+    assert sorted(btf_hip.ABI_SYMBOLS) == header_symbols()
+
+
+def test_exported_names_are_only_the_abi():
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    out = subprocess.run([nm, "-D", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    exported = sorted({l.split()[-1] for l in out.splitlines() if l.split() and l.split()[-1].startswith("btf_")})
+    assert exported == header_symbols()
+
+
+def test_pure_host_queries():
+    import btf_hip
+    assert btf_hip.gemv_max_nb(5120) > 0
+    assert btf_hip.gemv_max_nb(100) == 0
+    assert btf_hip.gemv_max_nb(0) == 0
+    prev = btf_hip.gemv_set_policy(7)
+    assert btf_hip.gemv_set_policy(prev) == 7
+
+
+def test_invalid_arguments_rejected_on_host():
+    """Every one of these fails in the host-side checks (no device exists in
+    this process, so reaching a HIP call would give another code)."""
+    import btf_hip as h
+    ARGS = h.BTF_ERR_ARGS
+    codes, scales, y = 0x100000, 0x200000, 0x300000
+    act = h.Q8Act(0x400000, 0x500000, 0x600000)
+    seg = h.GemvSeg(codes, scales, 64, y, 64)
+    assert h.launch_gemv_raw([seg], 1, 100, 1, act, 0) == ARGS                       # K % 128
+    assert h.launch_gemv_raw([seg], 0, 1024, 1, act, 0) == ARGS                      # no segment
+    assert h.launch_gemv_raw([seg] * 3, 4, 1024, 1, act, 0) == ARGS                  # > 3 segments
+    assert h.launch_gemv_raw([seg], 1, 1024, 1, act, 9) == ARGS                      # mode
+    assert h.launch_gemv_raw([seg], 1, 1024, 1, act, 2) == ARGS                      # swiglu needs 2 segs
+    assert h.launch_gemv_raw([h.GemvSeg(codes + 4, scales, 64, y, 64)], 1, 1024, 1, act, 0) == ARGS  # align
+    assert h.launch_gemv_raw([h.GemvSeg(codes, scales, 64, None, 64)], 1, 1024, 1, act, 0) == ARGS  # null y
+    assert h.launch_gemv_raw([h.GemvSeg(codes, scales, 64, y, 32)], 1, 1024, 2, act, 0) == ARGS   # ldy < N
+    assert h.launch_gemv_raw([seg], 1, 1024, 1, h.Q8Act(0x400001, 0x500000, 0x600000), 0) == ARGS  # q align
+    assert "gemv" in h.last_error()
+    assert h.launch_repack_raw(codes, -1, codes, scales) == h.BTF_OK                 # empty: no-op
+    assert h.launch_repack_raw(codes + 2, 10, codes, scales) == ARGS                 # src alignment
+    assert h.launch_repack_raw(codes, 10, codes + 8, scales) == ARGS                 # codes alignment
+    assert h.launch_prep_raw(y, 100, 1, 100, None, 0.0, None, None, 0, act) == ARGS   # n % 32
+    assert h.launch_prep_raw(y, 64, 1, 128, None, 0.0, None, None, 0, act) == ARGS    # ldx < n
+    # step programs: every structural error is caught before the device is touched
+    G = h.GemvMode
+    vecs = [h.StepVec(1024, y), h.StepVec(1024, None)]
+    bad = [
+        h.StepGemv(G.kStore, 1024, 1024, codes, scales, 0, 0),
+        h.StepGemv(G.kStore, 1000, 1024, codes, scales, 0, 1),
+        h.StepGemv(G.kStore, 1024, 512, codes, scales, 0, 1),
+        h.StepGemv(G.kStore, 1024, 1024, codes, scales, 0, 5),
+        h.StepGemv(G.kSwiglu, 1024, 1024, codes, scales, 0, 1),
+        h.StepGemv(G.kStore, 1024, 1024, codes + 8, scales, 0, 1),
+        h.StepGemv(G.kStore, 1024, 1024, codes, scales, 1, 0),
+    ]
+    for b in bad:
+        assert h.step_create_raw(vecs, [b]) == ARGS, b
+    assert h.step_create_raw([], []) == ARGS
+
+
+def _compile_and_run(tmp_path, name, src, compiler, std):
+    cc = shutil.which(compiler)
+    if cc is None:
+        pytest.skip(f"{compiler} not available")
+    path = tmp_path / name
+    path.write_text(src)
+    exe = tmp_path / (name + ".bin")
+    subprocess.run([cc, std, "-Wall", "-Werror", "-I", INC, str(path), "-o", str(exe), "-L", PKG, "-lbtf_hip",
+                    f"-Wl,-rpath,{PKG}"], check=True, capture_output=True, text=True)
+    return subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+
+
+C_SRC = r"""
+#include <stdio.h>
+#include "btf/hip_abi.h"
+int main(void) {
+  btf_gemv_seg seg = {0, 0, 64, 0, 64};
+  btf_q8act a = {0, 0, 0};
+  int rc = btf_hip_launch_gemv(&seg, 1, 100, 1, &a, BTF_GEMV_STORE, NULL);
+  printf("%d %d %s\n", btf_hip_gemv_max_nb(5120) > 0, rc, btf_hip_last_error());
+  return rc == BTF_ERR_ARGS ? 0 : 1;
+}
+"""
+
+CPP_SRC = r"""
+#include <cstdio>
+#include <stdexcept>
+#include "btf/kernels.hpp"
+int main() {
+  btf::hip::GemvSeg seg;
+  seg.N = 64;
+  btf::hip::Q8Act a;
+  try {
+    btf::hip::launch_gemv(&seg, 1, 100, 1, a, btf::hip::kStore, nullptr);
+  } catch (const std::runtime_error& e) {
+    std::printf("threw: %s\n", e.what());
+    return btf::hip::gemv_max_nb(5120) > 0 ? 0 : 2;
+  }
+  return 1;
+}
+"""
+
+
+def test_c_header_compiles_links_and_validates(tmp_path):
+    r = _compile_and_run(tmp_path, "abi_c.c", C_SRC, "gcc", "-std=c11")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "multiple of 128" in r.stdout
+
+
+def test_cpp_mirror_throws_like_the_reference(tmp_path):
+    r = _compile_and_run(tmp_path, "abi_cpp.cpp", CPP_SRC, "g++", "-std=c++17")
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert r.stdout.startswith("threw: launch_gemv:")

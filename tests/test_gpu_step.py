@@ -1,0 +1,318 @@
+"""GPU tests of the decode-step program (btf_hip_step_*): a chain of GEMVs,
+each with the Q8 quantize of its input, run as one persistent launch.
+
+Bars:
+  * bit-exact against the same chain launched op by op (launch_prep without
+    norm/transform + launch_gemv, batch 1): the step kernel uses the same
+    dot products, the same per-1024-column-slice DPP reduction and the same
+    slice order, and its producer-side Q8 is the q8 kernel's arithmetic;
+  * each op within rel-RMS 1e-3 (and max error 1e-3 of max |ref|) of the
+    oracle (oracle Q8 + emulator GEMV of src/emu_decoder.cpp:143-165, SwiGLU)
+    applied to the step's own input vector.
+The chain mirrors a decoder layer's GEMVs (src/cuda/gpu_decoder.cu:452-486):
+QKV (store) reading the residual stream written by the layer before, o
+(+= residual), gate/up (swiglu) and down (+= residual). Gate/up read a fixed
+normed-input stand-in: without the model's RMSNorm a residual feeding them
+would grow quadratically and overflow within a few layers.
+"""
+import numpy as np
+import pytest
+
+from helpers import assert_close_1e3, random_mat
+
+pytestmark = pytest.mark.gpu
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def dev(a):
+    torch = _torch()
+    a = np.ascontiguousarray(a)
+    if a.dtype == np.uint16:
+        a = a.view(np.int16)
+    return torch.from_numpy(a.copy()).cuda()
+
+
+def host(t):
+    _torch().cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def stream():
+    return _torch().cuda.current_stream().cuda_stream
+
+
+class Mat:
+    """A packed matrix on the device (codes [N][K/4], scales [N][K/128])."""
+
+    def __init__(self, codes, scales, N, K, host_codes=None, host_scales=None):
+        self.codes, self.scales, self.N, self.K = codes, scales, N, K
+        self.host_codes, self.host_scales = host_codes, host_scales
+
+
+def host_mat(oracle, rng, N, K):
+    """Random weights with block scales ~0.03 (a GEMV then keeps the input's
+    magnitude order over a chain; with unit scales every op multiplies it by
+    ~20 and a few ops overflow the fp16 Q8 scale on the CPU and GPU alike)."""
+    c, s = random_mat(oracle, rng, N, K, scale=0.03)
+    return Mat(dev(c), dev(s), N, K, c, s)
+
+
+def gen_dev_mat(hip, N, K, mat_id, seed=7):
+    """Seeded generator + repack on the device (both bit-exact with the
+    oracle, see test_gpu_parity)."""
+    torch = _torch()
+    nb = N * K // 128
+    src = torch.empty(nb * 28, dtype=torch.uint8, device="cuda")
+    codes = torch.empty(N * K // 4, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(N * K // 128, dtype=torch.int16, device="cuda")
+    hip.gen_ptq1_0(seed, mat_id, 0, nb, src, stream())
+    hip.launch_repack(src, nb, codes, scales, stream())
+    torch.cuda.synchronize()
+    return Mat(codes, scales, N, K)
+
+
+def layer_ops(hip, mats, RES, QKV, ATT, H, X):
+    """The four GEMVs of one layer over vector slots RES, QKV, ATT, H, X."""
+    G = hip.GemvMode
+    qkv, o, gate, up, down = mats
+    return [
+        hip.StepGemv(G.kStore, qkv.K, qkv.N, qkv.codes, qkv.scales, RES, QKV),
+        hip.StepGemv(G.kAdd, o.K, o.N, o.codes, o.scales, ATT, RES),
+        hip.StepGemv(G.kSwiglu, gate.K, gate.N, gate.codes, gate.scales, X, H, up.codes, up.scales),
+        hip.StepGemv(G.kAdd, down.K, down.N, down.codes, down.scales, H, RES),
+    ]
+
+
+def run_sequential(hip, ops, vecs):
+    """The same chain launched op by op on torch tensors `vecs` (updated)."""
+    torch = _torch()
+    G = hip.GemvMode
+    for op in ops:
+        K = op.K
+        act = hip.Q8Act(torch.empty(K, dtype=torch.int8, device="cuda"),
+                        torch.empty(K // 32, dtype=torch.float32, device="cuda"),
+                        torch.empty(K // 32, dtype=torch.int32, device="cuda"))
+        hip.launch_prep(vecs[op.in_vec], K, 1, K, None, 0.0, None, None, 0, act, stream())
+        y = vecs[op.out_vec]
+        if op.mode == G.kSwiglu:
+            segs = [hip.GemvSeg(op.codes, op.scales, op.N, y, op.N), hip.GemvSeg(op.up_codes, op.up_scales, op.N, None, 0)]
+        else:
+            segs = [hip.GemvSeg(op.codes, op.scales, op.N, y, op.N)]
+        hip.launch_gemv(segs, K, 1, act, op.mode, stream())
+    torch.cuda.synchronize()
+
+
+def small_chain(hip, oracle, layers, H=1024, NQ=1000, F=3072, seed=5):
+    """Vectors: 0 = residual (input, += target), 1 = qkv output (N = 1000, not
+    a multiple of 32: a partial last unit), 2 = attention-output stand-in,
+    3 = MLP hidden, 4 = the normed-input stand-in. Random encoder-quantized
+    weights. (Step programs take K % 1024 == 0 and N % 4 == 0.)"""
+    rng = np.random.default_rng(seed)
+    res0 = rng.standard_normal(H).astype(np.float32)
+    att = (rng.standard_normal(H) * 2).astype(np.float32)
+    xin = rng.standard_normal(H).astype(np.float32)
+    ops, hm = [], []
+    for _ in range(layers):
+        mats = [host_mat(oracle, rng, NQ, H), host_mat(oracle, rng, H, H), host_mat(oracle, rng, F, H),
+                host_mat(oracle, rng, F, H), host_mat(oracle, rng, H, F)]
+        ops += layer_ops(hip, mats, 0, 1, 2, 3, 4)
+    return ops, (res0, att, xin), (H, NQ, F)
+
+
+def make_vectors(hip, inputs, dims, with_h_data=False):
+    torch = _torch()
+    res0, att, xin = inputs
+    H, NQ, F = dims
+    t = [dev(res0), torch.zeros(NQ, dtype=torch.float32, device="cuda"), dev(att),
+         torch.zeros(F, dtype=torch.float32, device="cuda"), dev(xin)]
+    vecs = [hip.StepVec(H, t[0]), hip.StepVec(NQ, t[1]), hip.StepVec(H, t[2]),
+            hip.StepVec(F, t[3] if with_h_data else None), hip.StepVec(H, t[4])]
+    return vecs, t
+
+
+@pytest.mark.parametrize("layers", [1, 3])
+def test_step_matches_sequential_small(hip, oracle, layers):
+    ops, inputs, dims = small_chain(hip, oracle, layers)
+    vecs, t = make_vectors(hip, inputs, dims, with_h_data=True)
+    prog = hip.StepProgram(vecs, ops)
+    prog.launch(stream())
+    _torch().cuda.synchronize()
+    assert prog.error() == 0
+    # sequential launches on fresh copies
+    _, s = make_vectors(hip, inputs, dims, with_h_data=True)
+    run_sequential(hip, ops, s)
+    for name, a, b in zip(("res", "qkv", "att", "h", "x"), t, s):
+        ga, gb = host(a), host(b)
+        assert np.isfinite(ga).all(), name
+        assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), \
+            f"{name}: step != sequential (max diff {np.max(np.abs(ga - gb)):.3e})"
+    prog.close()
+
+
+def test_step_each_op_vs_oracle(hip, oracle):
+    """Every op against the oracle on the step's own input vector: a chain in
+    which each op writes a vector of its own (all observable), so a Q8 input
+    that differs in the last float bit between GPU and CPU (and would round
+    one q the other way) cannot compound across ops."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(23)
+    H, F, N0 = 1024, 3072, 2048
+    W = [host_mat(oracle, rng, N0, H), host_mat(oracle, rng, H, N0), host_mat(oracle, rng, F, H),
+         host_mat(oracle, rng, F, H), host_mat(oracle, rng, H, F)]
+    x0 = rng.standard_normal(H).astype(np.float32)
+    r0 = rng.standard_normal(H).astype(np.float32)
+    r1 = rng.standard_normal(H).astype(np.float32)
+    # vectors: 0 = x (input), 1 = a (N0), 2 = r (+= target, H), 3 = h (F), 4 = out (+= target, H)
+    t = [dev(x0), torch.zeros(N0, dtype=torch.float32, device="cuda"), dev(r0),
+         torch.zeros(F, dtype=torch.float32, device="cuda"), dev(r1)]
+    vecs = [hip.StepVec(int(v.numel()), v) for v in t]
+    ops = [hip.StepGemv(G.kStore, H, N0, W[0].codes, W[0].scales, 0, 1),
+           hip.StepGemv(G.kAdd, N0, H, W[1].codes, W[1].scales, 1, 2),
+           hip.StepGemv(G.kSwiglu, H, F, W[2].codes, W[2].scales, 2, 3, W[3].codes, W[3].scales),
+           hip.StepGemv(G.kAdd, F, H, W[4].codes, W[4].scales, 3, 4)]
+    prog = hip.StepProgram(vecs, ops)
+    prog.launch(stream())
+    torch.cuda.synchronize()
+    assert prog.error() == 0
+    a, r, h, out = host(t[1]), host(t[2]), host(t[3]), host(t[4])
+
+    def q8(v):
+        return oracle.quantize_rows(np.ascontiguousarray(v[None, :]))
+
+    q, d, s = q8(x0)
+    assert_close_1e3(a, oracle.gemv(W[0].host_codes, W[0].host_scales, H, q, d, s)[0], "store")
+    q, d, s = q8(a)
+    assert_close_1e3(r, oracle.gemv(W[1].host_codes, W[1].host_scales, N0, q, d, s, y=r0[None, :].copy(),
+                                    add=True)[0], "add")
+    q, d, s = q8(r)
+    g = oracle.gemv(W[2].host_codes, W[2].host_scales, H, q, d, s)
+    u = oracle.gemv(W[3].host_codes, W[3].host_scales, H, q, d, s)
+    assert_close_1e3(h, oracle.swiglu(g, u)[0], "swiglu")
+    q, d, s = q8(h)
+    assert_close_1e3(out, oracle.gemv(W[4].host_codes, W[4].host_scales, F, q, d, s, y=r1[None, :].copy(),
+                                      add=True)[0], "add K=3072")
+    prog.close()
+
+
+def test_step_repeated_launches(hip, oracle):
+    """Three launches in a row continue the residual stream (the program's
+    epoch/tag progression): equal to three sequential passes."""
+    ops, inputs, dims = small_chain(hip, oracle, 2, seed=11)
+    vecs, t = make_vectors(hip, inputs, dims)
+    prog = hip.StepProgram(vecs, ops)
+    _, s = make_vectors(hip, inputs, dims, with_h_data=True)
+    for rep in range(3):
+        prog.launch(stream())
+        run_sequential(hip, ops, s)
+        _torch().cuda.synchronize()
+        assert prog.error() == 0
+        for name, i in (("res", 0), ("qkv", 1)):
+            assert np.array_equal(host(t[i]).view(np.uint32), host(s[i]).view(np.uint32)), f"launch {rep}: {name}"
+    prog.close()
+
+
+def test_step_27b_layer_and_output(hip):
+    """One 27B layer (QKV 5120->7168, o 5120->5120, gate/up 5120->17408,
+    down 17408->5120) plus the output projection 5120->248320 in one launch,
+    bit-exact against the op-by-op launches."""
+    torch = _torch()
+    E, F, QKV, V = 5120, 17408, 7168, 248320
+    mats = [gen_dev_mat(hip, QKV, E, 1), gen_dev_mat(hip, E, E, 2), gen_dev_mat(hip, F, E, 3),
+            gen_dev_mat(hip, F, E, 4), gen_dev_mat(hip, E, F, 5)]
+    out = gen_dev_mat(hip, V, E, 6)
+    ops = layer_ops(hip, mats, 0, 1, 2, 3, 5)
+    ops.append(hip.StepGemv(hip.GemvMode.kStore, E, V, out.codes, out.scales, 0, 4))
+    rng = np.random.default_rng(3)
+    res0 = rng.standard_normal(E).astype(np.float32)
+    att = rng.standard_normal(E).astype(np.float32)
+    xin = rng.standard_normal(E).astype(np.float32)
+
+    def vectors():
+        t = [dev(res0), torch.zeros(QKV, dtype=torch.float32, device="cuda"), dev(att),
+             torch.zeros(F, dtype=torch.float32, device="cuda"), torch.zeros(V, dtype=torch.float32, device="cuda"),
+             dev(xin)]
+        return [hip.StepVec(E, t[0]), hip.StepVec(QKV, t[1]), hip.StepVec(E, t[2]), hip.StepVec(F, t[3]),
+                hip.StepVec(V, t[4]), hip.StepVec(E, t[5])], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    prog.launch(stream())
+    torch.cuda.synchronize()
+    assert prog.error() == 0
+    _, s = vectors()
+    run_sequential(hip, ops, s)
+    for name, a, b in zip(("res", "qkv", "att", "h", "logits", "x"), t, s):
+        ga, gb = host(a), host(b)
+        assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), \
+            f"{name}: step != sequential (max diff {np.max(np.abs(ga - gb)):.3e})"
+    assert np.isfinite(host(t[4])).all() and np.abs(host(t[4])).max() > 0
+    prog.close()
+
+
+def test_step_timeout_sets_error_and_recovers(hip, oracle):
+    """A poll bound of 1 makes waiting workgroups give up (forced from the
+    host: every wait is bounded, every wave still exits). The launch reports
+    the error; with the default bound restored the next launch is exact."""
+    ops, inputs, dims = small_chain(hip, oracle, 2, seed=17)
+    res0 = inputs[0]
+    vecs, t = make_vectors(hip, inputs, dims)
+    prog = hip.StepProgram(vecs, ops)
+    prog.set_spin_limit(1)
+    prog.launch(stream())
+    _torch().cuda.synchronize()
+    err = prog.error()
+    assert prog.error() == 0, "error() clears the flag"
+    # restore inputs and the default bound; the next launch must be exact
+    t[0].copy_(dev(res0))
+    prog.set_spin_limit(0)
+    prog.launch(stream())
+    _, s = make_vectors(hip, inputs, dims, with_h_data=True)
+    run_sequential(hip, ops, s)
+    _torch().cuda.synchronize()
+    assert prog.error() == 0
+    for i in (0, 1):
+        assert np.array_equal(host(t[i]).view(np.uint32), host(s[i]).view(np.uint32))
+    # a launch with a 1-poll bound practically always has to wait longer
+    assert err in (0, 1)
+    prog.close()
+
+
+def test_step_invalid_programs(hip):
+    torch = _torch()
+    G = hip.GemvMode
+    codes = torch.zeros(1024 * 1024 // 4, dtype=torch.uint8, device="cuda")
+    scales = torch.zeros(1024 * 1024 // 128, dtype=torch.int16, device="cuda")
+    x = torch.zeros(1024, dtype=torch.float32, device="cuda")
+    v = [hip.StepVec(1024, x), hip.StepVec(1024, None)]
+    ok = hip.StepGemv(G.kStore, 1024, 1024, codes, scales, 0, 1)
+    assert hip.step_create_raw(v, [ok]) == hip.BTF_OK
+    bad = [
+        hip.StepGemv(G.kStore, 1024, 1024, codes, scales, 0, 0),           # reads its own output
+        hip.StepGemv(G.kStore, 1000, 1024, codes, scales, 0, 1),           # K % 128
+        hip.StepGemv(G.kStore, 1152, 1024, codes, scales, 0, 1),           # K % 1024
+        hip.StepGemv(G.kStore, 1024, 1022, codes, scales, 0, 1),           # N % 4 (and != length)
+        hip.StepGemv(G.kStore, 1024, 512, codes, scales, 0, 1),            # N != output length
+        hip.StepGemv(G.kStore, 1024, 1024, codes, scales, 0, 2),           # vector index
+        hip.StepGemv(7, 1024, 1024, codes, scales, 0, 1),                  # mode
+        hip.StepGemv(G.kStore, 1024, 1024, codes.data_ptr() + 4, scales, 0, 1),  # codes alignment
+        hip.StepGemv(G.kSwiglu, 1024, 1024, codes, scales, 0, 1),          # swiglu without up
+        hip.StepGemv(G.kStore, 1024, 1024, codes, scales, 1, 0),           # reads vector 1 before any write (no data)
+    ]
+    for b in bad:
+        assert hip.step_create_raw(v, [b]) == hip.BTF_ERR_ARGS, b
+        assert hip.last_error()
+    # quantized vector of a length that is not a multiple of 32
+    v2 = [hip.StepVec(1000, x), hip.StepVec(1024, None)]
+    assert hip.step_create_raw(v2, [hip.StepGemv(G.kStore, 896, 1024, codes, scales, 0, 1)]) == hip.BTF_ERR_ARGS
+    # K beyond the widest supported input
+    big = [hip.StepVec(24576, x), hip.StepVec(1024, None)]
+    assert hip.step_create_raw(big, [hip.StepGemv(G.kStore, 24576, 1024, codes, scales, 0, 1)]) == hip.BTF_ERR_ARGS
+    # output too tall for the per-workgroup partial buffer (nothing is launched)
+    tall = [hip.StepVec(20480, x), hip.StepVec(131072, None)]
+    assert hip.step_create_raw(tall, [hip.StepGemv(G.kStore, 20480, 131072, codes, scales, 0, 1)]) == \
+        hip.BTF_ERR_ARGS
