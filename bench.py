@@ -365,6 +365,8 @@ def main():
                     help="auto: at batch 1 both engines are timed and the faster one is the value; "
                          "the graph otherwise")
     ap.add_argument("--no-kinds", action="store_true", help="skip the per-GEMV-kind graph timings")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="first run 3 device copies of 1 GiB (the scale reference for HBM counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -381,6 +383,15 @@ def main():
     hip.kernels_init(0)
     info = hip.device_info(0)
     log(f"device {info['name']} {info['gcn_arch']} CUs={info['cu_count']}")
+
+    if args.calib_copy:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("calibration: 3 device copies of 1 GiB (reads 1 GiB, writes 1 GiB each)")
+        del a, b
 
     layers = args.layers if args.workload == "sweep" else (1 if args.workload == "layer" else 8)
     t0 = time.time()
