@@ -2,19 +2,21 @@
 """Benchmark of the fused ternary matmul path on one MI355X.
 
 Default workload: the 27B-scale decode-step weight sweep at batch 1 --
-64 layers x (QKV 5120->7168, o 5120->5120 (+= residual), gate+up
-5120->17408 as one swiglu GEMV, down 17408->5120 (+= residual)) plus the
+64 layers x (QKV 5120->7168, o 5120->5120, gate+up 5120->17408 as one
+swiglu GEMV, down 17408->5120 (+= residual)) plus the
 untied output projection 5120->248,320, every GEMV fed by the Q8 quantize of
 its input. 5,952,839,680 B of packed codes + scales per step, seeded
 synthetic weights (trits p = 0.3/0.4/0.3, fp16 scales U[0.01, 0.05]) and
 N(0,1) activations.
 
 Data flow of a layer (the same for both engines): QKV reads the residual
-stream, o adds W_o * (attention-output stand-in) into it, gate/up read the
-normed-input stand-in x, down adds W_down * h into it; the output
-projection reads the final residual. (Without the model's RMSNorm a residual
-feeding gate/up would grow quadratically and overflow; this keeps every
-value finite while still chaining every layer through the residual.)
+stream (written by the previous layer's down), o writes W_o * (attention-
+output stand-in) to x, gate/up read x, down adds W_down * h into the
+residual; the output projection reads the final residual. Every GEMV but o
+waits for the one before it, as in the decoder; o's input stands in for
+the attention output, which is outside this path. (Without the model's
+RMSNorm, o adding into the residual that gate/up read would grow
+quadratically and overflow; o storing into x keeps every value finite.)
 
 Engines:
   step  (default at batch 1): the whole GEMV chain as ONE persistent launch
@@ -129,7 +131,7 @@ class Step:
         self.S, self.M, self.layers = S, M, layers
         rng = np.random.default_rng(0)
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
-        self.x = dev(rng.standard_normal((M, E)).astype(np.float32))     # normed hidden state stand-in
+        self.x = torch.zeros((M, E), dtype=torch.float32, device="cuda")  # FFN input (o-proj output)
         self.xo = dev(rng.standard_normal((M, E)).astype(np.float32))    # attention-output stand-in
         self.res0 = rng.standard_normal((M, E)).astype(np.float32)       # residual stream at step start
         self.res = dev(self.res0)
@@ -142,7 +144,7 @@ class Step:
                              torch.zeros((M, Kmax // 32), dtype=torch.int32, device="cuda"))
         self.with_output = with_output
         # algorithmic bytes
-        b_gemv = {"qkv": gemv_bytes(QKV, E, M), "o": gemv_bytes(E, E, M, 2), "gateup": gemv_bytes(F, E, M, 1, 2),
+        b_gemv = {"qkv": gemv_bytes(QKV, E, M), "o": gemv_bytes(E, E, M), "gateup": gemv_bytes(F, E, M, 1, 2),
                   "down": gemv_bytes(E, F, M, 2), "output": gemv_bytes(V, E, 1)}
         self.kind_bytes = b_gemv
         self.gemv_bytes = layers * (b_gemv["qkv"] + b_gemv["o"] + b_gemv["gateup"] + b_gemv["down"])
@@ -167,7 +169,7 @@ class Step:
         self.prep(self.res, E, M, st)
         self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
         self.prep(self.xo, E, M, st)
-        self.gemv([S.seg("o", l, self.res, E)], E, M, G.kAdd, st)
+        self.gemv([S.seg("o", l, self.x, E)], E, M, G.kStore, st)
         self.prep(self.x, E, M, st)
         self.gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, G.kSwiglu, st)
         self.prep(self.h, F, M, st)
@@ -198,12 +200,14 @@ class Step:
             N, K, _, co, so = S.mats[(name, l)]
             return base + co, base + so
 
+        # The op-by-op order; every op waits for the one before it, except o,
+        # whose input stands in for the attention output.
         ops = []
         for l in range(self.layers):
-            ops.append(hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1))
-            ops.append(hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0))
             gc, gs = w("gate", l)
             uc, us = w("up", l)
+            ops.append(hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1))
+            ops.append(hip.StepGemv(G.kStore, E, E, *w("o", l), 2, 3))
             ops.append(hip.StepGemv(G.kSwiglu, E, F, gc, gs, 3, 4, uc, us))
             ops.append(hip.StepGemv(G.kAdd, F, E, *w("down", l), 4, 0))
         if self.with_output:
@@ -216,7 +220,7 @@ class Step:
         if kind == "qkv":
             self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
         elif kind == "o":
-            self.gemv([S.seg("o", l, self.res, E)], E, M, G.kAdd, st)
+            self.gemv([S.seg("o", l, self.x, E)], E, M, G.kStore, st)
         elif kind == "gateup":
             self.gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, G.kSwiglu, st)
         elif kind == "down":
@@ -276,7 +280,7 @@ def verify_step_vs_graph(torch, step: Step, prog):
         torch.cuda.synchronize()
         run(torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
-        outs.append([t.cpu().numpy().copy() for t in (step.res, step.qkv, step.h, step.logits) if t is not None])
+        outs.append([t.cpu().numpy().copy() for t in (step.res, step.qkv, step.x, step.h, step.logits) if t is not None])
     if prog.error():
         return False, "step program reported a timeout"
     for a, b in zip(*outs):

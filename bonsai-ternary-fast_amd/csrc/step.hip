@@ -38,6 +38,7 @@
 //    workgroup) records an error and lets every wave run to completion.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <climits>
 #include <cstring>
 #include <vector>
@@ -59,6 +60,7 @@ constexpr int kMaxPart = 8192;              // partial sums per op per workgroup
 constexpr int kMaxOps = 384;                // ops per program (descriptors live in LDS)
 constexpr int kMaxOld = 1024;               // rows per workgroup of an add-mode op (old values in LDS)
 constexpr int kWordsPerBlock = 10;          // LL words per 32-value Q8 block
+constexpr int kSlots = 3;                   // LL buffers of each kind per vector (versions in turn)
 constexpr uint32_t kSpinMax = 1u << 20;     // poll bound (each poll is a memory round trip: ~1 s)
 
 // 144 bytes (a multiple of 16: copied into LDS in 16-byte words).
@@ -75,7 +77,11 @@ struct OpDev {
   uint32_t in_tag;           // relative tag of the input's producer
   uint32_t old_tag;          // add mode: relative tag of the output's previous version
   uint32_t my_tag;
-  int pad0, pad1;
+  uint8_t early;      // 1: the I/O waves fetch this op's input during the previous op
+  uint8_t carry_in;   // 1: add-mode old values come from the previous op's epilogue (LDS carry)
+  uint8_t carry_out;  // 1: the epilogue keeps its outputs in the LDS carry for the next op
+  uint8_t pad0;
+  int pad1;
   const uint8_t* codes;
   const uint16_t* scales;
   const uint8_t* up_codes;
@@ -111,14 +117,17 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 struct Lds {
   OpDev opd[kMaxOps];        // the program
-  uint32_t act_q[kMaxK / 4];  // q bytes of the current op's input
-  float act_d[kMaxK / 32];    // d
-  int32_t act_s[kMaxK / 32];  // s
+  uint32_t act_q[2][kMaxK / 4];  // q bytes of an op's input (by op parity)
+  float act_d[2][kMaxK / 32];    // d
+  int32_t act_s[2][kMaxK / 32];  // s
   float part[kMaxPart];       // [local row][1024-column slice]
   float oldv[2][kMaxOld];     // add mode: previous values of the workgroup's rows (by op parity)
+  float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
   uint32_t epoch;
   uint32_t abort_;
   uint32_t spin_max;
+  uint32_t cdone;             // compute waves done with their items, summed over the GEMVs so far
+  uint32_t fetched[kMaxOps];  // I/O waves that completed the early fetch of op i
 };
 
 __device__ __forceinline__ bool aborted(Lds& L) {
@@ -165,24 +174,25 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
 }
 
 // Fetch an op's input (its Q8 LL words, tag = the input producer's) into
-// LDS and, for add mode, the previous values of this workgroup's rows (tag =
-// the previous writer's) into L.oldv[ob], polling until every tag matches.
-// Run by the NL lanes of the compute waves (lane id lid) while the I/O waves
-// run the previous op's epilogue: with NL = 640 every input of up to 20480
-// values is one round of loads. The old-value loads are issued first and
-// checked last, so their round trip overlaps the input's.
-template <int NL>
-__device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ctl* ctl, uint32_t base_tag, int wg, int G,
-                                            int ob) {
-  constexpr int kIn = (kMaxK / 32 * kWordsPerBlock + NL - 1) / NL;  // input words per lane
-  constexpr int kOld = (kMaxOld + NL - 1) / NL;                      // old values per lane
+// LDS buffer `ob` and, for add mode without carry, the previous values of
+// this workgroup's rows (tag = the previous writer's) into L.oldv[ob],
+// polling until every tag matches. NL lanes (lane id lid) take words
+// lid + k*NL in rounds of B words per lane. The old-value loads are issued
+// first and checked last, so their round trip overlaps the input's.
+// stop_at != 0: give up (return false) once L.cdone reaches stop_at (the
+// compute waves have finished the op this fetch was overlapping).
+template <int NL, int B>
+__device__ __forceinline__ bool fetch_input(const OpDev& op, Lds& L, int lid, Ctl* ctl, uint32_t base_tag, int wg, int G,
+                                            int ob, uint32_t stop_at = 0) {
+  constexpr int kOld = (kMaxOld + NL - 1) / NL;  // old values per lane
   const uint64_t* in = sgpr_ptr(op.in_q8);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
   const uint64_t* old = sgpr_ptr(op.old_f32);
   const uint32_t told = base_tag + sgpr(op.old_tag);
   const int first = first_unit(sgpr(op.rot), wg, G);
-  const int nold = sgpr(op.mode) == BTF_GEMV_ADD ? units_of(sgpr(op.units), first, G) * 32 : 0;
+  const int nold =
+      (sgpr(op.mode) == BTF_GEMV_ADD && !sgpr(op.carry_in)) ? units_of(sgpr(op.units), first, G) * 32 : 0;
   const int N = sgpr(op.N);
   uint64_t vo[kOld];
 #pragma unroll
@@ -191,43 +201,51 @@ __device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ct
     const int row = (first + (k >> 5) * G) * 32 + (k & 31);
     vo[b] = (k < nold && row < N) ? ll_load(old + row) : ((uint64_t)told << 32);
   }
-  uint64_t v[kIn];
+  for (int base = lid; base < nin; base += B * NL) {
+    uint64_t v[B];
 #pragma unroll
-  for (int b = 0; b < kIn; ++b) {
-    const int idx = lid + b * NL;
-    v[b] = idx < nin ? ll_load(in + idx) : ((uint64_t)tin << 32);
+    for (int b = 0; b < B; ++b) {
+      const int idx = base + b * NL;
+      v[b] = idx < nin ? ll_load(in + idx) : ((uint64_t)tin << 32);
+    }
+    uint32_t spins = 0;
+    for (;;) {
+      uint32_t pending = 0;
+#pragma unroll
+      for (int b = 0; b < B; ++b) pending |= ((uint32_t)(v[b] >> 32) != tin) ? (1u << b) : 0u;
+      if (pending == 0) break;
+      if (stop_at && __hip_atomic_load(&L.cdone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= stop_at)
+        return false;
+      if (!poll_step(spins, L, ctl)) break;
+#pragma unroll
+      for (int b = 0; b < B; ++b)
+        if (pending & (1u << b)) v[b] = ll_load(in + base + b * NL);
+    }
+#pragma unroll
+    for (int b = 0; b < B; ++b) {
+      const int idx = base + b * NL;
+      if (idx < nin) {
+        const uint32_t data = (uint32_t)v[b];
+        const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
+        if (w < 8)
+          L.act_q[ob][blk * 8 + w] = data;
+        else if (w == 8)
+          L.act_d[ob][blk] = __uint_as_float(data);
+        else
+          L.act_s[ob][blk] = (int32_t)data;
+      }
+    }
   }
+  if (nold == 0) return true;
   uint32_t spins = 0;
   for (;;) {
     uint32_t pending = 0;
 #pragma unroll
-    for (int b = 0; b < kIn; ++b) pending |= ((uint32_t)(v[b] >> 32) != tin) ? (1u << b) : 0u;
-    if (pending == 0 || !poll_step(spins, L, ctl)) break;
-#pragma unroll
-    for (int b = 0; b < kIn; ++b)
-      if (pending & (1u << b)) v[b] = ll_load(in + lid + b * NL);
-  }
-#pragma unroll
-  for (int b = 0; b < kIn; ++b) {
-    const int idx = lid + b * NL;
-    if (idx < nin) {
-      const uint32_t data = (uint32_t)v[b];
-      const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
-      if (w < 8)
-        L.act_q[blk * 8 + w] = data;
-      else if (w == 8)
-        L.act_d[blk] = __uint_as_float(data);
-      else
-        L.act_s[blk] = (int32_t)data;
-    }
-  }
-  if (nold == 0) return;
-  spins = 0;
-  for (;;) {
-    uint32_t pending = 0;
-#pragma unroll
     for (int b = 0; b < kOld; ++b) pending |= ((uint32_t)(vo[b] >> 32) != told) ? (1u << b) : 0u;
-    if (pending == 0 || !poll_step(spins, L, ctl)) break;
+    if (pending == 0) break;
+    if (stop_at && __hip_atomic_load(&L.cdone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= stop_at)
+      return false;
+    if (!poll_step(spins, L, ctl)) break;
 #pragma unroll
     for (int b = 0; b < kOld; ++b) {
       if (pending & (1u << b)) {
@@ -241,6 +259,7 @@ __device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ct
     const int k = lid + b * NL;
     if (k < nold) L.oldv[ob][k] = __uint_as_float((uint32_t)vo[b]);  // rows past N: unused
   }
+  return true;
 }
 
 // ---------------------------------------------------------------- compute waves
@@ -375,10 +394,10 @@ __device__ __forceinline__ void issue_item(const OpR& op, const LaneAddr& la, in
 // The activation of this lane's chunk of slice s (64 q bytes, d/16, -s of
 // its two sub-blocks). The 4 row groups of a wave read the same addresses
 // (LDS broadcasts).
-__device__ __forceinline__ void load_act(const Lds& L, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
+__device__ __forceinline__ void load_act(const Lds& L, int ob, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
                                          int (&an)[2]) {
   const int chunk = s * 16 + l16;
-  const u32x4* qp = reinterpret_cast<const u32x4*>(&L.act_q[chunk * 16]);
+  const u32x4* qp = reinterpret_cast<const u32x4*>(&L.act_q[ob][chunk * 16]);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const u32x4 v = qp[i];
@@ -387,8 +406,8 @@ __device__ __forceinline__ void load_act(const Lds& L, int s, int l16, uint32_t 
     aq[4 * i + 2] = v.z;
     aq[4 * i + 3] = v.w;
   }
-  const float2 d = *reinterpret_cast<const float2*>(&L.act_d[2 * chunk]);
-  const int2 sv = *reinterpret_cast<const int2*>(&L.act_s[2 * chunk]);
+  const float2 d = *reinterpret_cast<const float2*>(&L.act_d[ob][2 * chunk]);
+  const int2 sv = *reinterpret_cast<const int2*>(&L.act_s[ob][2 * chunk]);
   ad[0] = d.x * 0.0625f;  // exact: the dot returns 16 * I
   ad[1] = d.y * 0.0625f;
   an[0] = -sv.x;
@@ -472,7 +491,12 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     }
   }
   for (;;) {
-    fetch_input<64 * kCW>(L.opd[cur.i], L, wave * 64 + lane, ctl, base_tag, wg, G, cur.i & 1);
+    const int ob = cur.i & 1;  // LDS buffers of this op
+    // not fetched (completely) by the I/O waves during the previous op
+    if (!sgpr(L.opd[cur.i].early) ||
+        __hip_atomic_load(&L.fetched[cur.i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (uint32_t)kIW)
+      fetch_input<64 * kCW, (kMaxK / 32 * kWordsPerBlock + 64 * kCW - 1) / (64 * kCW)>(L.opd[cur.i], L, wave * 64 + lane,
+                                                                                       ctl, base_tag, wg, G, ob);
     lds_barrier();  // A: the op's input is in LDS
     const int R = cur.Q * 4;  // rows (virtual: swiglu gate/up interleaved) of this workgroup
     Cur cc{cur.s0, cur.q0};   // entry being consumed
@@ -482,7 +506,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     uint32_t aq[16];
     float ad[2];
     int an[2];
-    load_act(L, cc.s, l16, aq, ad, an);
+    load_act(L, ob, cc.s, l16, aq, ad, an);
     const int nb = cur.P / kRing;
     for (int b = 0; b < nb - 1; ++b) {
 #pragma unroll
@@ -496,7 +520,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         finish(c, ad, e < cur.n, cc.s * R + cc.q * 4 + grp, l16, L);
         const int s_prev = cc.s;
         cur_next(cur.Q, cc);
-        if (cc.s != s_prev) load_act(L, cc.s, l16, aq, ad, an);
+        if (cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
     {  // last batch: the refills load the next op's first entries
@@ -512,9 +536,10 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         finish(c, ad, e < cur.n, cc.s * R + cc.q * 4 + grp, l16, L);
         const int s_prev = cc.s;
         cur_next(cur.Q, cc);
-        if (r + 1 < kRing && cc.s != s_prev) load_act(L, cc.s, l16, aq, ad, an);
+        if (r + 1 < kRing && cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
+    if (lane == 0) (void)__hip_atomic_fetch_add(&L.cdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     lds_barrier();  // B: the op's partial sums are in LDS
     if (nxt.i >= nops) break;
     cur = nxt;
@@ -607,6 +632,7 @@ __device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int
   const int S = (sgpr(op.cpr) + 15) >> 4;  // 1024-column slices: partial sums per row
   const int R = nunits * (mode == BTF_GEMV_SWIGLU ? 64 : 32);  // rows of part[slice][row]
   const uint32_t tag = base_tag + sgpr(op.my_tag);
+  const bool carry_in = sgpr(op.carry_in), carry_out = sgpr(op.carry_out);
   for (int ui = half; ui < nunits; ui += nhalves) {
     const int unit = first + ui * G;
     const int row = unit * 32 + j;
@@ -624,7 +650,8 @@ __device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int
       const int lr = ui * 32 + j;
       float sum = 0.f;
       for (int k = 0; k < S; ++k) sum += L.part[k * R + lr];
-      v = mode == BTF_GEMV_ADD ? L.oldv[ob][lr] + sum : sum;
+      v = mode == BTF_GEMV_ADD ? (carry_in ? L.carry[lr] : L.oldv[ob][lr]) + sum : sum;
+      if (carry_out) L.carry[lr] = v;
     }
     publish_unit(op, unit, j, valid ? v : 0.f, valid, tag);
   }
@@ -632,15 +659,28 @@ __device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int
 
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
                                          uint32_t base_tag) {
+  uint32_t gi = 0;  // GEMVs so far (the compute waves' done count reaches gi * kCW)
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
     if (sgpr(op.kind) == 0) {
       io_quantize(op, wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
-    lds_barrier();  // A: the compute waves have fetched the op's input into LDS
+    lds_barrier();  // A: the op's input is in LDS
     if (sgpr(op.count_reads) && iol == 0)
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // While the compute waves work on op i: fetch the next op's input when
+    // its producers are all before op i (then no workgroup waits on op i).
+    // It gives up when the compute waves are done with op i (B must not
+    // wait for it); the compute waves then fetch the input themselves.
+    const int nx = sgpr(op.next);
+    ++gi;
+    if (nx < nops && sgpr(L.opd[nx].early)) {
+      const bool done = fetch_input<64 * kIW, 16>(L.opd[nx], L, iol, ctl, base_tag, wg, G, nx & 1, gi * kCW);
+      // per wave: all of its lanes completed their share
+      if (__builtin_amdgcn_readfirstlane(__builtin_amdgcn_ballot_w64(!done) == 0) && (iol & 63) == 0)
+        (void)__hip_atomic_fetch_add(&L.fetched[nx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
     wait_readers(sgpr(op.war_op), rd_cnt, G, L, ctl);
     lds_barrier();  // B: the compute waves' partial sums are in LDS
     io_epilogue(op, L, wg, G, iol, base_tag, i & 1);
@@ -660,7 +700,9 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
     const int nvec = nops * (int)(sizeof(OpDev) / 16);
     for (int k = threadIdx.x; k < nvec; k += kThreads) dst[k] = src[k];
   }
+  for (int k = threadIdx.x; k < nops; k += kThreads) L.fetched[k] = 0;
   if (threadIdx.x == 0) {
+    L.cdone = 0;
     L.epoch = ctl_load(&ctl->epoch);
     const uint32_t sm = ctl_load(&ctl->spin_max);
     L.spin_max = sm ? sm : kSpinMax;
@@ -780,22 +822,93 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     step_destroy(P);
     return fail(code, msg);
   };
-  std::vector<uint64_t*> f32(nvec, nullptr), q8(nvec, nullptr);
-  for (int v = 0; v < nvec; ++v) {
-    if (needs_f32[v] && !(f32[v] = static_cast<uint64_t*>(alloc((size_t)vecs[v].n * 8))))
-      return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
-    if (needs_q8[v] && !(q8[v] = static_cast<uint64_t*>(alloc((size_t)(vecs[v].n / 32) * kWordsPerBlock * 8))))
-      return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
+  // ---- versions of every vector over the program (pre-pass). Version 0 of a
+  // vector read before any write is its user data, quantized by a prologue
+  // op; every GEMV writes a new version of its output vector. A version gets
+  // Q8 LL words only if a later op reads it as input; every GEMV output gets
+  // fp32 LL words (read by a later add-mode op as its old value, or not).
+  struct Version {
+    int writer;                 // GEMV index, -1 = prologue
+    int last_q8_reader = -1;    // GEMV index
+    std::vector<int> f32_readers;
+    int q8_slot = -1, f32_slot = -1;
+  };
+  std::vector<std::vector<Version>> versions(nvec);
+  std::vector<int> op_in_ver(ngemv), op_old_ver(ngemv, -1), op_out_ver(ngemv);
+  for (int v = 0; v < nvec; ++v)
+    if (needs_init[v]) versions[v].push_back(Version{-1});
+  for (int i = 0; i < ngemv; ++i) {
+    const btf_step_gemv& g = gemvs[i];
+    op_in_ver[i] = (int)versions[g.in_vec].size() - 1;
+    versions[g.in_vec].back().last_q8_reader = i;
+    if (g.mode == BTF_GEMV_ADD) {
+      op_old_ver[i] = (int)versions[g.out_vec].size() - 1;
+      versions[g.out_vec].back().f32_readers.push_back(i);
+    }
+    op_out_ver[i] = (int)versions[g.out_vec].size();
+    versions[g.out_vec].push_back(Version{i});
   }
+  // kSlots buffers of each kind per vector, taken in turn by the versions
+  // that need one, so a version overwrites the one kSlots such versions
+  // earlier (whose readers have long finished, normally).
+  std::vector<uint64_t*> f32buf[kSlots], q8buf[kSlots];
+  for (int b = 0; b < kSlots; ++b) {
+    f32buf[b].assign(nvec, nullptr);
+    q8buf[b].assign(nvec, nullptr);
+  }
+  for (int v = 0; v < nvec; ++v) {
+    int nq = 0, nf = 0;
+    for (Version& ve : versions[v]) {
+      if (ve.last_q8_reader >= 0) ve.q8_slot = nq++ % kSlots;
+      // every GEMV's result is written to device memory (fp32 words), read
+      // later or not; the prologue's version 0 only if an add reads it
+      if (ve.writer >= 0 || !ve.f32_readers.empty()) ve.f32_slot = nf++ % kSlots;
+    }
+    for (int b = 0; b < kSlots && b < nq; ++b)
+      if (!(q8buf[b][v] = static_cast<uint64_t*>(alloc((size_t)(vecs[v].n / 32) * kWordsPerBlock * 8))))
+        return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
+    for (int b = 0; b < kSlots && b < nf; ++b)
+      if (!(f32buf[b][v] = static_cast<uint64_t*>(alloc((size_t)vecs[v].n * 8))))
+        return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
+  }
+  auto q8_of = [&](int v, int k) { return versions[v][k].q8_slot >= 0 ? q8buf[versions[v][k].q8_slot][v] : nullptr; };
+  auto f32_of = [&](int v, int k) { return versions[v][k].f32_slot >= 0 ? f32buf[versions[v][k].f32_slot][v] : nullptr; };
   // ---- the device program: prologue quantize ops, then the GEMVs in order
   std::vector<OpDev> ops;
-  std::vector<int> last_writer(nvec, -1);  // device op index of the current version's producer
-  std::vector<int> last_reader(nvec, -1);  // last GEMV that read the current version's Q8
-  int rot = 0;
-  auto add_units = [&](OpDev& o) {
+  std::vector<int> dev_of(ngemv, -1);        // device op index of each GEMV
+  std::vector<int> prologue_of(nvec, -1);    // device op index of each prologue op
+  // Unit placement: unit u of an op goes to workgroup (u + rot) % G. An
+  // add-mode op takes the rotation of the op that wrote its old value when
+  // they have the same units, so each row's old value was published by the
+  // same workgroup (no cross-workgroup wait on an add chain). Any other op
+  // takes the rotation that keeps the most-loaded workgroup's weight bytes
+  // lowest.
+  std::vector<double> load(G, 0.0);
+  auto place = [&](OpDev& o, double cost_per_unit, int align_to) {
     o.units = (o.N + 31) / 32;
-    o.rot = rot % G;
-    rot = (rot + o.units) % G;
+    const int extra = o.units % G;
+    int best = 0;
+    if (align_to >= 0 && ops[align_to].units == o.units) {
+      best = ops[align_to].rot;
+    } else if (extra) {
+      // the `extra` workgroups with one more unit form a window of length
+      // extra starting at rot: pick the window with the least load
+      double best_max = 1e300;
+      for (int r = 0; r < G; ++r) {
+        double mx = 0.0;
+        for (int k = 0; k < extra; ++k) mx = std::max(mx, load[(r + k) % G]);
+        if (mx < best_max) {
+          best_max = mx;
+          best = r;
+        }
+      }
+    }
+    o.rot = best;
+    for (int w = 0; w < G; ++w) {
+      const int first = (w - best + G) % G;
+      const int n = first < o.units ? (o.units - 1 - first) / G + 1 : 0;
+      load[w] += n * cost_per_unit;
+    }
   };
   for (int v = 0; v < nvec; ++v) {
     if (!needs_init[v]) continue;
@@ -803,17 +916,22 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     o.kind = 0;
     o.N = vecs[v].n;
     o.src = vecs[v].data;
-    o.out_f32 = f32[v];
-    o.out_q8 = q8[v];
+    o.out_q8 = q8_of(v, 0);
+    o.out_f32 = f32_of(v, 0);
     o.my_tag = (uint32_t)ops.size() + 1;
     o.war_op = -1;
-    add_units(o);
-    last_writer[v] = (int)ops.size();
+    place(o, 1.0, -1);
+    prologue_of[v] = (int)ops.size();
     ops.push_back(o);
   }
+  auto dev_writer = [&](int v, int k) {
+    const int w = versions[v][k].writer;
+    return w < 0 ? prologue_of[v] : dev_of[w];
+  };
   for (int i = 0; i < ngemv; ++i) {
     const btf_step_gemv& g = gemvs[i];
     const int me = (int)ops.size();
+    dev_of[i] = me;
     OpDev o{};
     o.kind = 1;
     o.mode = g.mode;
@@ -825,37 +943,87 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     o.scales = g.scales;
     o.up_codes = g.up_codes;
     o.up_scales = g.up_scales;
-    o.in_q8 = q8[g.in_vec];
-    o.in_tag = (uint32_t)last_writer[g.in_vec] + 1;
-    // Only the final version goes to the user's buffer: plain stores of two
-    // ops to one address from different XCDs would reach HBM in the order
-    // their L2s write back, not in program order.
-    o.out_plain = final_writer[g.out_vec] == i ? vecs[g.out_vec].data : nullptr;
-    o.out_f32 = f32[g.out_vec];
-    o.out_q8 = q8[g.out_vec];
+    o.in_q8 = q8_of(g.in_vec, op_in_ver[i]);
+    o.in_tag = (uint32_t)dev_writer(g.in_vec, op_in_ver[i]) + 1;
+    int align_to = -1;
     if (g.mode == BTF_GEMV_ADD) {
-      o.old_f32 = f32[g.out_vec];
-      o.old_tag = (uint32_t)last_writer[g.out_vec] + 1;
+      o.old_f32 = f32_of(g.out_vec, op_old_ver[i]);
+      o.old_tag = (uint32_t)dev_writer(g.out_vec, op_old_ver[i]) + 1;
+      align_to = dev_writer(g.out_vec, op_old_ver[i]);
     }
+    const int kv = op_out_ver[i];
+    const Version& nv = versions[g.out_vec][kv];
+    // Plain output: only the final version goes to the user's buffer (plain
+    // stores of two ops to one address from different XCDs reach HBM in the
+    // order their L2s write back, not in program order).
+    o.out_plain = final_writer[g.out_vec] == i ? vecs[g.out_vec].data : nullptr;
+    o.out_q8 = q8_of(g.out_vec, kv);
+    o.out_f32 = f32_of(g.out_vec, kv);
     o.my_tag = (uint32_t)me + 1;
-    add_units(o);
-    // Replacing a version that GEMVs have read (its Q8 words, or the user
-    // data a prologue op quantized): wait for every workgroup's fetch of the
-    // last such reader's input.
-    o.war_op = last_reader[g.out_vec];
-    if (o.war_op >= 0) ops[o.war_op].count_reads = 1;
+    place(o, (double)g.K * (g.mode == BTF_GEMV_SWIGLU ? 2 : 1), align_to);
+    // Write-after-read: the buffers this version takes held the version
+    // kSlots such versions earlier; wait until every workgroup has fetched the
+    // input of its last reader. Old-value reads by an op with the same unit
+    // placement are reads of the workgroup's own rows, already ordered by
+    // program order. The final writer also stores into the user's buffer,
+    // which the prologue read (version 0): after every reader of version 0.
+    int war = -1;
+    for (int k = kv - 1; k >= 0; --k) {
+      const Version& pv = versions[g.out_vec][k];
+      if (nv.q8_slot >= 0 && pv.q8_slot == nv.q8_slot) {
+        war = std::max(war, pv.last_q8_reader >= 0 ? dev_of[pv.last_q8_reader] : -1);
+        break;
+      }
+    }
+    for (int k = kv - 1; k >= 0; --k) {
+      const Version& pv = versions[g.out_vec][k];
+      if (nv.f32_slot >= 0 && pv.f32_slot == nv.f32_slot) {
+        for (int r : pv.f32_readers) {
+          const OpDev& ro = ops[dev_of[r]];
+          if (!(ro.units == o.units && ro.rot == o.rot)) war = std::max(war, dev_of[r]);
+        }
+        break;
+      }
+    }
+    if (o.out_plain && needs_init[g.out_vec]) {
+      const Version& v0 = versions[g.out_vec][0];
+      int last = v0.last_q8_reader;
+      for (int r : v0.f32_readers) last = std::max(last, r);
+      if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
+    }
+    o.war_op = war;
+    if (war >= 0) ops[war].count_reads = 1;
     // per-workgroup LDS bounds: partial sums, old values of add-mode rows
     const int max_units = (o.units + G - 1) / G;
     const int rows = max_units * (g.mode == BTF_GEMV_SWIGLU ? 64 : 32);
     if (rows * ((o.cpr + 15) / 16) > kMaxPart) return bail(BTF_ERR_ARGS, "step: output too tall for the partial-sum buffer");
     if (g.mode == BTF_GEMV_ADD && max_units * 32 > kMaxOld)
       return bail(BTF_ERR_ARGS, "step: add-mode output too tall for the old-value buffer");
-    last_reader[g.in_vec] = me;
-    last_writer[g.out_vec] = me;
-    last_reader[g.out_vec] = -1;
     ops.push_back(o);
   }
   if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 384 ops (quantize prologue + GEMVs)");
+  // Early fetch and carry. An op's input is fetched by the I/O waves while
+  // the previous GEMV computes when every producer it reads from comes
+  // before that previous GEMV (a workgroup then never waits for its own
+  // unpublished output). An add-mode op whose old value was produced by the
+  // previous GEMV with the same unit placement takes it from the LDS carry
+  // (the same workgroup computed it).
+  {
+    int pd = -1;  // previous GEMV in program order
+    for (int d = 0; d < (int)ops.size(); ++d) {
+      OpDev& o = ops[d];
+      if (o.kind != 1) continue;
+      if (o.mode == BTF_GEMV_ADD && pd >= 0 && (int)o.old_tag - 1 == pd && ops[pd].units == o.units &&
+          ops[pd].rot == o.rot) {
+        o.carry_in = 1;
+        ops[pd].carry_out = 1;
+      }
+      const bool in_ok = (int)o.in_tag - 1 < pd;
+      const bool old_ok = o.mode != BTF_GEMV_ADD || o.carry_in || (int)o.old_tag - 1 < pd;
+      o.early = pd >= 0 && in_ok && old_ok;
+      pd = d;
+    }
+  }
   // next GEMV after each op
   {
     int nxt = (int)ops.size();
@@ -924,3 +1092,4 @@ int step_error(StepProgram* P, int* err) {
 }
 
 }  // namespace btfhip
+

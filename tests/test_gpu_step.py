@@ -153,6 +153,51 @@ def test_step_matches_sequential_small(hip, oracle, layers):
     prog.close()
 
 
+def test_step_reordered_chain_and_war(hip, oracle):
+    """The bench's program order (gate/up, QKV, o, down per layer: each op's
+    input produced two or three ops earlier, versions double-buffered) equals
+    the op-by-op launches; plus a vector read through the launch's quantize
+    prologue and then overwritten by a STORE as its final writer (the plain
+    store must wait for every read of the user's data)."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(31)
+    H, NQ, F = 1024, 1000, 3072
+    ops = []
+    for _ in range(3):
+        qkv, o, gate, up, down = (host_mat(oracle, rng, NQ, H), host_mat(oracle, rng, H, H), host_mat(oracle, rng, F, H),
+                                  host_mat(oracle, rng, F, H), host_mat(oracle, rng, H, F))
+        ops += [hip.StepGemv(G.kSwiglu, H, F, gate.codes, gate.scales, 4, 3, up.codes, up.scales),
+                hip.StepGemv(G.kStore, H, NQ, qkv.codes, qkv.scales, 0, 1),
+                hip.StepGemv(G.kAdd, H, H, o.codes, o.scales, 2, 0),
+                hip.StepGemv(G.kAdd, F, H, down.codes, down.scales, 3, 0)]
+    # vector 5 (data) is read by an op, then overwritten by a STORE (version 1, final)
+    w5a, w5b = host_mat(oracle, rng, H, H), host_mat(oracle, rng, H, H)
+    ops += [hip.StepGemv(G.kStore, H, H, w5a.codes, w5a.scales, 5, 6),
+            hip.StepGemv(G.kStore, H, H, w5b.codes, w5b.scales, 4, 5)]
+    inputs = [rng.standard_normal(n).astype(np.float32) for n in (H, NQ, H, F, H, H, H)]
+
+    def vectors():
+        t = [dev(a) for a in inputs]
+        return [hip.StepVec(int(x.numel()), x) for x in t], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    for rep in range(2):
+        if rep:
+            for x, a in zip(t, inputs):
+                x.copy_(dev(a))
+        prog.launch(stream())
+        torch.cuda.synchronize()
+        assert prog.error() == 0
+        _, s = vectors()
+        run_sequential(hip, ops, s)
+        for k, (a, b) in enumerate(zip(t, s)):
+            ga, gb = host(a), host(b)
+            assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), f"launch {rep} vector {k}"
+    prog.close()
+
+
 def test_step_each_op_vs_oracle(hip, oracle):
     """Every op against the oracle on the step's own input vector: a chain in
     which each op writes a vector of its own (all observable), so a Q8 input
