@@ -102,11 +102,14 @@ struct Ctl {
   uint32_t spin_max;  // poll bound of every wait; 0 = kSpinMax
 };
 
+// Through global (not flat) instructions: flat ones also count in lgkmcnt,
+// so every LDS barrier would wait for the LL round trips in flight.
+typedef __attribute__((address_space(1))) uint64_t gu64;
 __device__ __forceinline__ uint64_t ll_load(const uint64_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __hip_atomic_load((const gu64*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void ll_store(uint64_t* p, uint64_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_store((gu64*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ uint32_t ctl_load(const uint32_t* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -126,8 +129,6 @@ struct Lds {
   uint32_t epoch;
   uint32_t abort_;
   uint32_t spin_max;
-  uint32_t cdone;             // compute waves done with their items, summed over the GEMVs so far
-  uint32_t fetched[kMaxOps];  // I/O waves that completed the early fetch of op i
 };
 
 __device__ __forceinline__ bool aborted(Lds& L) {
@@ -179,11 +180,9 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
 // polling until every tag matches. NL lanes (lane id lid) take words
 // lid + k*NL in rounds of B words per lane. The old-value loads are issued
 // first and checked last, so their round trip overlaps the input's.
-// stop_at != 0: give up (return false) once L.cdone reaches stop_at (the
-// compute waves have finished the op this fetch was overlapping).
 template <int NL, int B>
-__device__ __forceinline__ bool fetch_input(const OpDev& op, Lds& L, int lid, Ctl* ctl, uint32_t base_tag, int wg, int G,
-                                            int ob, uint32_t stop_at = 0) {
+__device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ctl* ctl, uint32_t base_tag, int wg, int G,
+                                            int ob) {
   constexpr int kOld = (kMaxOld + NL - 1) / NL;  // old values per lane
   const uint64_t* in = sgpr_ptr(op.in_q8);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
@@ -214,8 +213,6 @@ __device__ __forceinline__ bool fetch_input(const OpDev& op, Lds& L, int lid, Ct
 #pragma unroll
       for (int b = 0; b < B; ++b) pending |= ((uint32_t)(v[b] >> 32) != tin) ? (1u << b) : 0u;
       if (pending == 0) break;
-      if (stop_at && __hip_atomic_load(&L.cdone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= stop_at)
-        return false;
       if (!poll_step(spins, L, ctl)) break;
 #pragma unroll
       for (int b = 0; b < B; ++b)
@@ -236,15 +233,13 @@ __device__ __forceinline__ bool fetch_input(const OpDev& op, Lds& L, int lid, Ct
       }
     }
   }
-  if (nold == 0) return true;
+  if (nold == 0) return;
   uint32_t spins = 0;
   for (;;) {
     uint32_t pending = 0;
 #pragma unroll
     for (int b = 0; b < kOld; ++b) pending |= ((uint32_t)(vo[b] >> 32) != told) ? (1u << b) : 0u;
     if (pending == 0) break;
-    if (stop_at && __hip_atomic_load(&L.cdone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= stop_at)
-      return false;
     if (!poll_step(spins, L, ctl)) break;
 #pragma unroll
     for (int b = 0; b < kOld; ++b) {
@@ -259,7 +254,58 @@ __device__ __forceinline__ bool fetch_input(const OpDev& op, Lds& L, int lid, Ct
     const int k = lid + b * NL;
     if (k < nold) L.oldv[ob][k] = __uint_as_float((uint32_t)vo[b]);  // rows past N: unused
   }
-  return true;
+}
+
+// The input fetch split in two for the I/O waves (kIW waves, one round, no
+// old values): the loads of an op whose input is at most kIL * kEIn words are
+// issued while the previous op computes and finished (poll what was stale,
+// write LDS) after that op's partial sums are in; its compute waves then
+// skip the fetch.
+constexpr int kIL = 64 * kIW;
+constexpr int kEIn = 13;  // input words per lane: K <= 5324
+struct EarlyFetch {
+  uint64_t v[kEIn];
+};
+__device__ __forceinline__ void early_issue(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f) {
+  const uint64_t* in = sgpr_ptr(op.in_q8);
+  const uint32_t tin = base_tag + sgpr(op.in_tag);
+  const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
+#pragma unroll
+  for (int b = 0; b < kEIn; ++b) {
+    const int idx = lid + b * kIL;
+    f.v[b] = idx < nin ? ll_load(in + idx) : ((uint64_t)tin << 32);
+  }
+}
+__device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, Lds& L, int ob,
+                                             Ctl* ctl) {
+  const uint64_t* in = sgpr_ptr(op.in_q8);
+  const uint32_t tin = base_tag + sgpr(op.in_tag);
+  const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
+  uint32_t spins = 0;
+  for (;;) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int b = 0; b < kEIn; ++b) pending |= ((uint32_t)(f.v[b] >> 32) != tin) ? (1u << b) : 0u;
+    if (pending == 0) break;
+    if (!poll_step(spins, L, ctl)) break;
+#pragma unroll
+    for (int b = 0; b < kEIn; ++b)
+      if (pending & (1u << b)) f.v[b] = ll_load(in + lid + b * kIL);
+  }
+#pragma unroll
+  for (int b = 0; b < kEIn; ++b) {
+    const int idx = lid + b * kIL;
+    if (idx < nin) {
+      const uint32_t data = (uint32_t)f.v[b];
+      const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
+      if (w < 8)
+        L.act_q[ob][blk * 8 + w] = data;
+      else if (w == 8)
+        L.act_d[ob][blk] = __uint_as_float(data);
+      else
+        L.act_s[ob][blk] = (int32_t)data;
+    }
+  }
 }
 
 // ---------------------------------------------------------------- compute waves
@@ -492,9 +538,8 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
   }
   for (;;) {
     const int ob = cur.i & 1;  // LDS buffers of this op
-    // not fetched (completely) by the I/O waves during the previous op
-    if (!sgpr(L.opd[cur.i].early) ||
-        __hip_atomic_load(&L.fetched[cur.i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != (uint32_t)kIW)
+    // (an early op's input was fetched by the I/O waves before this barrier)
+    if (!sgpr(L.opd[cur.i].early))
       fetch_input<64 * kCW, (kMaxK / 32 * kWordsPerBlock + 64 * kCW - 1) / (64 * kCW)>(L.opd[cur.i], L, wave * 64 + lane,
                                                                                        ctl, base_tag, wg, G, ob);
     lds_barrier();  // A: the op's input is in LDS
@@ -523,7 +568,14 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         if (cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
-    {  // last batch: the refills load the next op's first entries
+    if (cur.n == 0) {  // no real entry: only the refills with the next op's first entries
+      Cur ln{nxt.s0, nxt.q0};
+#pragma unroll
+      for (int r = 0; r < kRing; ++r) {
+        issue_item(nxt.op, la_nxt, nxt.first, ln, r < nxt.n, G, ring[r]);
+        cur_next(nxt.Q, ln);
+      }
+    } else {  // last batch: the refills load the next op's first entries
       Cur ln{nxt.s0, nxt.q0};
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
@@ -539,7 +591,6 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         if (r + 1 < kRing && cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
-    if (lane == 0) (void)__hip_atomic_fetch_add(&L.cdone, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     lds_barrier();  // B: the op's partial sums are in LDS
     if (nxt.i >= nops) break;
     cur = nxt;
@@ -554,20 +605,32 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
 // Q8 of 32 values held by a 32-lane half-wave (lane j holds value j), identical
 // to the q8 kernel / include/btf/packed.hpp:117-134. Returns q of this lane;
 // d and s valid in every lane of the half.
+// The reductions run in DPP within 16-lane rows, then v_permlane16_swap
+// combines rows 0/1 and 2/3 (no LDS traffic).
+__device__ __forceinline__ float half32_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ int half32_sum(int v) {
+  v += dpp_i<0xB1>(v);
+  v += dpp_i<0x4E>(v);
+  v += dpp_i<0x141>(v);
+  v += dpp_i<0x140>(v);
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  return (int)r[0] + (int)r[1];
+}
 __device__ __forceinline__ int q8_half(float v, float& d, int& s) {
-  float amax = fabsf(v);
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 32));
-  const float last = __shfl(v, 31, 32);
+  const float amax = half32_max(fabsf(v));
   float dd = h2f(f2h_bits(amax / 127.0f));
-  if (amax == 0.f) dd = copysignf(0.f, last);
+  if (amax == 0.f) dd = copysignf(0.f, __shfl(v, 31, 32));  // all 32 lanes of the half take this branch
   d = dd;
   const float id = amax != 0.f ? 127.0f / amax : 0.f;
   const int q = (int)__builtin_rintf(v * id);
-  int sum = q;
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) sum += __shfl_xor(sum, o, 32);
-  s = sum;
+  s = half32_sum(q);
   return q;
 }
 
@@ -578,7 +641,7 @@ __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, f
   float* out_plain = sgpr_ptr(op.out_plain);
   uint64_t* out_f32 = sgpr_ptr(op.out_f32);
   uint64_t* out_q8 = sgpr_ptr(op.out_q8);
-  if (valid && out_plain) out_plain[row] = v;
+  if (valid && out_plain) *(__attribute__((address_space(1))) float*)(out_plain + row) = v;
   if (valid && out_f32) ll_store(out_f32 + row, ((uint64_t)tag << 32) | __float_as_uint(v));
   if (out_q8) {
     float d;
@@ -586,8 +649,8 @@ __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, f
     const int q = q8_half(v, d, s);
     // pack 4 consecutive q bytes into one word (lanes 4w..4w+3)
     const uint32_t b = (uint32_t)(q & 0xff) << (8 * (j & 3));
-    uint32_t w = b | __shfl_xor(b, 1, 32);
-    w |= __shfl_xor(w, 2, 32);
+    uint32_t w = b | (uint32_t)dpp_i<0xB1>((int)b);  // quad_perm(1,0,3,2)
+    w |= (uint32_t)dpp_i<0x4E>((int)w);              // quad_perm(2,3,0,1)
     uint64_t* dst = out_q8 + (size_t)unit * kWordsPerBlock;
     if ((j & 3) == 0) ll_store(dst + (j >> 2), ((uint64_t)tag << 32) | w);
     if (j == 0) ll_store(dst + 8, ((uint64_t)tag << 32) | __float_as_uint(d));
@@ -603,7 +666,7 @@ __device__ __forceinline__ void io_quantize(const OpDev& op, int wg, int G, int 
   for (int u = first_unit(sgpr(op.rot), wg, G) + half * G; u < units; u += nhalves * G) {
     const int row = u * 32 + j;
     const bool valid = row < N;
-    const float v = valid ? src[row] : 0.f;
+    const float v = valid ? *(const __attribute__((address_space(1))) float*)(src + row) : 0.f;
     publish_unit(op, u, j, v, valid, tag);
   }
 }
@@ -659,7 +722,6 @@ __device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int
 
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
                                          uint32_t base_tag) {
-  uint32_t gi = 0;  // GEMVs so far (the compute waves' done count reaches gi * kCW)
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
     if (sgpr(op.kind) == 0) {
@@ -669,20 +731,16 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     lds_barrier();  // A: the op's input is in LDS
     if (sgpr(op.count_reads) && iol == 0)
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // While the compute waves work on op i: fetch the next op's input when
-    // its producers are all before op i (then no workgroup waits on op i).
-    // It gives up when the compute waves are done with op i (B must not
-    // wait for it); the compute waves then fetch the input themselves.
+    // The next op's input, when its producers all come before op i (no
+    // workgroup then waits on op i): loads issued while op i computes,
+    // finished after B (its buffer is free then), before op i's epilogue.
     const int nx = sgpr(op.next);
-    ++gi;
-    if (nx < nops && sgpr(L.opd[nx].early)) {
-      const bool done = fetch_input<64 * kIW, 16>(L.opd[nx], L, iol, ctl, base_tag, wg, G, nx & 1, gi * kCW);
-      // per wave: all of its lanes completed their share
-      if (__builtin_amdgcn_readfirstlane(__builtin_amdgcn_ballot_w64(!done) == 0) && (iol & 63) == 0)
-        (void)__hip_atomic_fetch_add(&L.fetched[nx], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
+    const bool early = nx < nops && sgpr(L.opd[nx].early);
+    EarlyFetch ef;
+    if (early) early_issue(L.opd[nx], iol, base_tag, ef);
     wait_readers(sgpr(op.war_op), rd_cnt, G, L, ctl);
     lds_barrier();  // B: the compute waves' partial sums are in LDS
+    if (early) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl);
     io_epilogue(op, L, wg, G, iol, base_tag, i & 1);
   }
 }
@@ -700,9 +758,7 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
     const int nvec = nops * (int)(sizeof(OpDev) / 16);
     for (int k = threadIdx.x; k < nvec; k += kThreads) dst[k] = src[k];
   }
-  for (int k = threadIdx.x; k < nops; k += kThreads) L.fetched[k] = 0;
   if (threadIdx.x == 0) {
-    L.cdone = 0;
     L.epoch = ctl_load(&ctl->epoch);
     const uint32_t sm = ctl_load(&ctl->spin_max);
     L.spin_max = sm ? sm : kSpinMax;
@@ -875,6 +931,14 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
   auto f32_of = [&](int v, int k) { return versions[v][k].f32_slot >= 0 ? f32buf[versions[v][k].f32_slot][v] : nullptr; };
   // ---- the device program: prologue quantize ops, then the GEMVs in order
   std::vector<OpDev> ops;
+  // seen[w]: the last GEMV whose input workgroup w has surely fetched before
+  // any workgroup passes the current op's input barrier. A workgroup passes
+  // an op's input barrier after every word of its input was published, and
+  // each publisher w had fetched the inputs of every op up to that producer
+  // first; a workgroup passes the barriers of all earlier ops before this
+  // one, so what they implied holds too (a running maximum).
+  std::vector<int> seen(G, -1);
+  auto owns = [&](const OpDev& x, int w) { return (w - x.rot + G) % G < x.units; };
   std::vector<int> dev_of(ngemv, -1);        // device op index of each GEMV
   std::vector<int> prologue_of(nvec, -1);    // device op index of each prologue op
   // Unit placement: unit u of an op goes to workgroup (u + rot) % G. An
@@ -991,6 +1055,15 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
       for (int r : v0.f32_readers) last = std::max(last, r);
       if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
     }
+    {
+      const int x = (int)o.in_tag - 1;  // input producer
+      int low = INT_MAX;
+      for (int w = 0; w < G; ++w) {
+        if (ops[x].kind == 1 && owns(ops[x], w)) seen[w] = std::max(seen[w], x);
+        low = std::min(low, seen[w]);
+      }
+      if (war >= 0 && low >= war) war = -1;  // implied by the barriers passed so far
+    }
     o.war_op = war;
     if (war >= 0) ops[war].count_reads = 1;
     // per-workgroup LDS bounds: partial sums, old values of add-mode rows
@@ -1019,8 +1092,9 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
         ops[pd].carry_out = 1;
       }
       const bool in_ok = (int)o.in_tag - 1 < pd;
-      const bool old_ok = o.mode != BTF_GEMV_ADD || o.carry_in || (int)o.old_tag - 1 < pd;
-      o.early = pd >= 0 && in_ok && old_ok;
+      const bool no_old = o.mode != BTF_GEMV_ADD || o.carry_in;
+      const bool fits = (o.K / 32) * kWordsPerBlock <= kIL * kEIn;  // one round of the I/O waves
+      o.early = pd >= 0 && in_ok && no_old && fits;
       pd = d;
     }
   }
