@@ -18,13 +18,17 @@ the attention output, which is outside this path. (Without the model's
 RMSNorm, o adding into the residual that gate/up read would grow
 quadratically and overflow; o storing into x keeps every value finite.)
 
-Engines:
-  step  (default at batch 1): the whole GEMV chain as ONE persistent launch
-        (btf_hip_step_*), each op's Q8 input produced by its producer;
+Engines (at batch 1 all three are timed; the fastest gives `value`):
+  step : the whole GEMV chain as ONE persistent launch (btf_hip_step_*),
+         each op's Q8 input produced by its producer;
+  chain: one hipGraph of GEMV launches with most quantizes fused in
+         (btf_hip_launch_gemv_ex: QKV, o and gate/up quantize their own fp32
+         inputs; down and the output projection keep a quantize launch);
   graph: one hipGraph of quantize + GEMV launches (2 per GEMV), as the
-        reference decoder captures its step.
-The step engine's outputs are checked bit-exact against the graph engine's
-before timing ("verified" in the JSON line).
+         reference decoder captures its step.
+The step and chain engines' outputs are checked bit-exact against the graph
+engine's before timing ("verified" in the JSON line). All engines are rated
+on the same algorithmic bytes of the workload.
 
 `value` = algorithmic bytes of one step / measured step time (weights,
 activations and outputs already resident in HBM), in GB/s.
@@ -175,6 +179,26 @@ class Step:
         self.prep(self.h, F, M, st)
         self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
 
+    def layer_chain(self, l, st):
+        """The same layer with most quantizes inside the GEMV launches
+        (btf_hip_launch_gemv_ex): QKV, o and gate/up quantize their fp32
+        inputs themselves; down's 17408-wide input keeps its own quantize
+        launch (re-reading it in every GEMV workgroup costs more)."""
+        S, M, G, hip = self.S, self.M, self.S.hip.GemvMode, self.S.hip
+        hip.launch_gemv_ex([S.seg("qkv", l, self.qkv, QKV)], E, M, x=self.res, ldx=E, mode=G.kStore, stream=st)
+        hip.launch_gemv_ex([S.seg("o", l, self.x, E)], E, M, x=self.xo, ldx=E, mode=G.kStore, stream=st)
+        hip.launch_gemv_ex([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, x=self.x, ldx=E,
+                           mode=G.kSwiglu, stream=st)
+        self.prep(self.h, F, M, st)
+        self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
+
+    def run_chain(self, st):
+        for l in range(self.layers):
+            self.layer_chain(l, st)
+        if self.with_output:
+            self.prep(self.res, E, 1, st)
+            self.gemv([self.S.seg("output", self.layers, self.logits, V)], E, 1, self.S.hip.GemvMode.kStore, st)
+
     def run(self, st):
         for l in range(self.layers):
             self.layer(l, st)
@@ -214,9 +238,17 @@ class Step:
             ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 5))
         return hip.StepProgram(vecs, ops)
 
-    def kind_launch(self, kind, l, st):
-        """One GEMV launch of a given kind (for per-kernel timing)."""
+    def kind_launch(self, kind, l, st, fused=False):
+        """One GEMV launch of a given kind (for per-kernel timing); fused: the
+        launch of the chain engine (quantizes fused in)."""
         S, M, G = self.S, self.M, self.S.hip.GemvMode
+        if fused and kind in ("qkv", "o", "gateup"):  # as in run_chain
+            x, segs, mode = {
+                "qkv": (self.res, [S.seg("qkv", l, self.qkv, QKV)], G.kStore),
+                "o": (self.xo, [S.seg("o", l, self.x, E)], G.kStore),
+                "gateup": (self.x, [S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], G.kSwiglu)}[kind]
+            S.hip.launch_gemv_ex(segs, E, M, x=x, ldx=E, mode=mode, stream=st)
+            return
         if kind == "qkv":
             self.gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, G.kStore, st)
         elif kind == "o":
@@ -270,19 +302,18 @@ def time_program(hip, torch, prog, reps, warmup):
     return e0.elapsed_ms(e1) / reps
 
 
-def verify_step_vs_graph(torch, step: Step, prog):
-    """Bit-exact comparison of one step-program launch with the op-by-op
-    launches of the same chain from the same residual."""
+def verify_vs_graph(torch, step: Step, runner):
+    """Bit-exact comparison of one run of another engine (a step-program
+    launch, or the fused launches) with the op-by-op launches of the same
+    chain from the same residual."""
     import numpy as np
     outs = []
-    for run in (lambda st: step.run(st), lambda st: prog.launch(st)):
+    for run in (lambda st: step.run(st), runner):
         step.reset()
         torch.cuda.synchronize()
         run(torch.cuda.current_stream().cuda_stream)
         torch.cuda.synchronize()
         outs.append([t.cpu().numpy().copy() for t in (step.res, step.qkv, step.x, step.h, step.logits) if t is not None])
-    if prog.error():
-        return False, "step program reported a timeout"
     for a, b in zip(*outs):
         if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
             return False, f"max |diff| {float(np.max(np.abs(a - b))):.3e}"
@@ -365,8 +396,8 @@ def main():
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
-    ap.add_argument("--engine", default="auto", choices=["auto", "step", "graph"],
-                    help="auto: at batch 1 both engines are timed and the faster one is the value; "
+    ap.add_argument("--engine", default="auto", choices=["auto", "step", "chain", "graph"],
+                    help="auto: at batch 1 every engine is timed and the fastest one is the value; "
                          "the graph otherwise")
     ap.add_argument("--no-kinds", action="store_true", help="skip the per-GEMV-kind graph timings")
     ap.add_argument("--calib-copy", action="store_true",
@@ -411,31 +442,43 @@ def main():
     else:
         step = Step(S, 512, layers, with_output=False)
 
-    engines = [args.engine] if args.engine != "auto" else (["step", "graph"] if step.M == 1 else ["graph"])
-    if "step" in engines and step.M != 1:
-        raise SystemExit("the step engine runs batch-1 chains only")
+    engines = [args.engine] if args.engine != "auto" else (["step", "chain", "graph"] if step.M == 1 else ["graph"])
+    if ("step" in engines or "chain" in engines) and step.M != 1:
+        raise SystemExit("the step and chain engines run batch-1 chains only")
 
-    verified = None
+    verified = {}
     engine_ms = {}
     if "step" in engines:
         t0 = time.time()
         prog = step.program()
         log(f"step program built in {time.time() - t0:.2f} s")
-        ok, why = verify_step_vs_graph(torch, step, prog)
-        verified = {"vs_graph_engine": ok, "detail": why}
+        ok, why = verify_vs_graph(torch, step, lambda st: prog.launch(st))
+        if prog.error():
+            ok, why = False, "step program reported a timeout"
+        verified["step"] = why
         log(f"step program vs op-by-op launches: {why}")
         if not ok:
             raise SystemExit(f"step program does not match the op-by-op launches: {why}")
         step.reset()
         engine_ms["step"] = time_program(hip, torch, prog, args.steps, args.warmup)
         log(f"step engine: {engine_ms['step']:.4f} ms per step")
+    if "chain" in engines:
+        ok, why = verify_vs_graph(torch, step, lambda st: step.run_chain(st))
+        verified["chain"] = why
+        log(f"chain launches vs op-by-op launches: {why}")
+        if not ok:
+            raise SystemExit(f"chain launches do not match the op-by-op launches: {why}")
+        step.reset()
+        engine_ms["chain"], _ = time_graph(hip, torch, step.run_chain, args.steps, args.warmup)
+        log(f"chain engine: {engine_ms['chain']:.4f} ms per step")
     if "graph" in engines:
         step.reset()
         engine_ms["graph"], g = time_graph(hip, torch, step.run, args.steps, args.warmup)
         log(f"graph engine: {engine_ms['graph']:.4f} ms per step")
     engine = min(engine_ms, key=engine_ms.get)
     ms = engine_ms[engine]
-    kernels_per_step = 1 if engine == "step" else layers * 8 + (2 if step.with_output else 0)
+    kernels_per_step = {"step": 1, "chain": layers * 5 + (2 if step.with_output else 0)}.get(
+        engine, layers * 8 + (2 if step.with_output else 0))
     log(f"{engine} engine reported: {ms:.4f} ms per step ({step.total_bytes / 1e9:.4f} GB algorithmic)")
     value = step.total_bytes / (ms / 1e3) / 1e9
 
@@ -443,11 +486,12 @@ def main():
     # layer (distinct weights) -> average per launch.
     kinds = ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else [])
     per = {}
-    if not args.no_kinds or engine == "graph":
+    fk = engine == "chain"
+    if not args.no_kinds or engine != "step":
         for kind in kinds:
             reps = 1 if kind == "output" else layers
-            fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st)) if kind == "output" else \
-                 (lambda st, kind=kind: [step.kind_launch(kind, l, st) for l in range(layers)])
+            fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st, fk)) if kind == "output" else \
+                 (lambda st, kind=kind: [step.kind_launch(kind, l, st, fk) for l in range(layers)])
             kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
             avg_us = kms * 1e3 / reps
             b = step.kind_bytes[kind]
@@ -465,7 +509,8 @@ def main():
         if step.M <= 32:
             roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
-                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'})",
+                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'}"
+                              f"{', quantizes fused in' if fk else ''})",
                     "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
         else:
             K_ = F if dom == "down" else E
@@ -505,7 +550,7 @@ def main():
         "frac_of_8TBs": round(value / HBM_PEAK_GBS, 4),
         "tok_s_equiv": round(1e3 / ms, 2) if args.workload == "sweep" else None,
         "roofline": roof,
-        "verified": verified,
+        "verified": {"vs_graph_engine_bit_exact": verified} if verified else None,
         "engines_ms": {k: round(v, 4) for k, v in engine_ms.items()},
         "gemv_kinds": per,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},

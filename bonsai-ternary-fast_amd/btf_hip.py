@@ -74,6 +74,8 @@ _launch_repack = _decl("btf_hip_launch_repack", [_vp, _i64, _vp, _vp, _vp])
 _launch_prep = _decl("btf_hip_launch_prep",
                      [_vp, _i, _i, _i, _vp, C.c_float, C.POINTER(_Hx), _vp, _i, C.POINTER(_Q8Act), _vp])
 _launch_gemv = _decl("btf_hip_launch_gemv", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _i, _vp])
+_launch_gemv_ex = _decl("btf_hip_launch_gemv_ex", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _vp, _i, _i,
+                                                    C.POINTER(_Q8Act), _vp])
 _dump = _decl("btf_hip_gemv_i32_dump", [_vp, _i, _i, _i, C.POINTER(_Q8Act), _vp, _vp])
 _set_policy = _decl("btf_hip_gemv_set_policy", [_i])
 _gen = _decl("btf_hip_gen_ptq1_0", [C.c_uint64, C.c_uint64, _i64, _i64, _vp, _vp])
@@ -99,7 +101,7 @@ _step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
 #: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
 ABI_SYMBOLS = (
     "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
-    "btf_hip_launch_gemv", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
+    "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
     "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
     "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
     "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
@@ -204,6 +206,21 @@ def launch_gemv(segs, K: int, M: int, a: Q8Act, mode: GemvMode = GemvMode.kStore
     arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs])
     q = a._c()
     _check(_launch_gemv(arr, len(segs), K, M, C.byref(q), int(mode), _stream(stream)))
+
+
+def launch_gemv_ex(segs, K: int, M: int, a: Q8Act = None, x=None, ldx: int = 0,
+                   mode: GemvMode = GemvMode.kStore, out: Q8Act = None, stream=None) -> None:
+    """launch_gemv with the chain's quantizes fused in (no reference
+    counterpart): input from Q8 rows `a` or fp32 rows `x` [M][ldx]; `out`
+    (optional) receives the Q8 rows of the output."""
+    _check(launch_gemv_ex_raw(segs, len(segs), K, M, a, x, ldx, int(mode), out, stream))
+
+
+def launch_gemv_ex_raw(segs, nseg: int, K: int, M: int, a, x, ldx: int, mode: int, out=None, stream=None) -> int:
+    arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs]) if segs else None
+    qa = C.byref(a._c()) if a is not None else None
+    qo = C.byref(out._c()) if out is not None else None
+    return _launch_gemv_ex(arr, nseg, K, M, qa, _addr(x), ldx, mode, qo, _stream(stream))
 
 
 def launch_gemv_raw(segs, nseg: int, K: int, M: int, a: Q8Act, mode: int, stream=None) -> int:

@@ -184,6 +184,36 @@ int btf_hip_launch_gemv(const btf_gemv_seg* segs, int nseg, int K, int M, const 
   return run_gemv(segs, nseg, K, M, a, mode, nullptr, static_cast<hipStream_t>(stream));
 }
 
+int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, const float* x,
+                           int ldx, int mode, const btf_q8act* out, btf_stream_t stream) {
+  if (M <= 0) return BTF_OK;
+  if ((a == nullptr) == (x == nullptr)) return fail(BTF_ERR_ARGS, "gemv_ex: give exactly one of a (Q8 rows) and x");
+  if (x && (!aligned(x, 16) || ldx < K || ldx % 4))
+    return fail(BTF_ERR_ARGS, "gemv_ex: x must be 16-byte aligned with ldx >= K and ldx % 4 == 0");
+  if (K > 32768) return fail(BTF_ERR_ARGS, "gemv_ex: K > 32768");
+  // the weight and output checks of launch_gemv (with x, the Q8 pointers are not read)
+  const btf_q8act none{reinterpret_cast<int8_t*>(16), reinterpret_cast<float*>(16), reinterpret_cast<int32_t*>(16)};
+  int rc = check_gemv(segs, nseg, K, M, a ? a : &none, mode, true);
+  if (rc != BTF_OK) return rc;
+  if (out) {
+    if ((rc = check_q8(out, "gemv_ex")) != BTF_OK) return rc;
+    if (mode != BTF_GEMV_SWIGLU && nseg != 1) return fail(BTF_ERR_ARGS, "gemv_ex: a Q8 output takes one segment");
+    if (segs[0].N % 32) return fail(BTF_ERR_ARGS, "gemv_ex: a Q8 output needs N % 32 == 0");
+  }
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  GemvSeg sg[3];
+  for (int i = 0; i < nseg; ++i) sg[i] = {segs[i].codes, segs[i].scales, segs[i].N, segs[i].y, segs[i].ldy};
+  const Q8 in = a ? Q8{a->q, a->d, a->s} : Q8{nullptr, nullptr, nullptr};
+  const Q8 qo = out ? Q8{out->q, out->d, out->s} : Q8{nullptr, nullptr, nullptr};
+  for (int m = 0; m < M; ++m) {
+    rc = gemv_dot4(sg, nseg, K, m, 1, in, mode, nullptr, static_cast<hipStream_t>(stream), *ds, x, ldx,
+                   out ? &qo : nullptr);
+    if (rc != BTF_OK) return rc;
+  }
+  return BTF_OK;
+}
+
 int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q8act* a, int32_t* I_out,
                           btf_stream_t stream) {
   if (M <= 0 || N <= 0) return BTF_OK;

@@ -20,6 +20,17 @@
 //    and does not depend on how slices are spread over waves, so the
 //    persistent step kernel, which walks the same slices, gives identical
 //    results.
+//  * QOUT (fused output quantize, one activation row): a workgroup owns one
+//    32-row block of the output (T = 8; swiglu T = 16), and its epilogue
+//    also writes the Q8 of that block (a half-wave per block, DPP
+//    reductions), so the next GEMV of a chain reads it without a quantize
+//    launch in between.
+//  * QIN (fused input quantize, one activation row): instead of reading Q8
+//    rows, each wave quantizes the fp32 input over its own K range (lane t:
+//    16*CL consecutive values, a 32-value block per lane pair or per lane)
+//    into LDS with the arithmetic of the q8 kernel, while the weight loads
+//    are in flight; the q/d/s it reads back are those a separate quantize
+//    launch would have written.
 #include <climits>
 
 #include "../../include/btf/hip_abi.h"
@@ -45,14 +56,82 @@ struct Dot4Args {
   const int32_t* s;
   int m0, nb;
   int32_t* dump;
+  const float* x;  // QIN: fp32 input rows
+  int ldx;
+  int8_t* oq;  // QOUT: Q8 rows of the output (q [.][N], d and s [.][N/32])
+  float* od;
+  int32_t* os;
 };
 
 constexpr int kMaxWaves = 16;
 
-template <int CL, int NB, int T, int MODE, bool DUMP>
-__global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
+// QIN: the Q8 of values [v0, v0 + 16*CL) of row x (0 past K) into this
+// wave's LDS region xw: words q, then d and s per 32-value block. CL == 1: a
+// block spans lanes 2u, 2u+1 (DPP quad_perm exchanges of amax, sum, last).
+// Same arithmetic as the q8 kernel: d = fp16_rn(amax/127), q = rint(x *
+// (127/amax)), s = sum q, all-zero block: d = +-0 with its last value's sign.
+// The lane's values, loaded before the weight stream is issued (loads return
+// in order: issued after it, they would arrive after the last weight).
+// A lane past K loads the row's first values (in bounds) and zeroes them in
+// quantize_lane.
+template <int CL>
+__device__ __forceinline__ void load_lane_x(const float* __restrict__ xrow, int v0, int K, float4 (&v)[4 * CL]) {
+  const float* p = xrow + (v0 < K ? v0 : 0);  // K % 128 == 0: the lane's range is all in or all out
+#pragma unroll
+  for (int i = 0; i < 4 * CL; ++i) v[i] = *reinterpret_cast<const float4*>(p + 4 * i);
+}
+template <int CL>
+__device__ __forceinline__ void quantize_lane(const float4 (&xv)[4 * CL], bool live, int lane, uint32_t* xw) {
+  constexpr int NV = 16 * CL;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < 4 * CL; ++i) {
+    v[4 * i] = live ? xv[i].x : 0.f;
+    v[4 * i + 1] = live ? xv[i].y : 0.f;
+    v[4 * i + 2] = live ? xv[i].z : 0.f;
+    v[4 * i + 3] = live ? xv[i].w : 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  float last = v[NV - 1];
+  if constexpr (CL == 1) {
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));  // quad_perm(1,0,3,2): the pair's other half
+    last = dpp_f<0xF5>(last);               // quad_perm(1,1,3,3): the odd lane holds the block's end
+  }
+  float d = h2f(f2h_bits(amax / 127.0f));
+  if (amax == 0.f) d = copysignf(0.f, last);
+  const float id = amax != 0.f ? 127.0f / amax : 0.f;
+  int sum = 0;
+  uint32_t wq[NV / 4];
+#pragma unroll
+  for (int k = 0; k < NV / 4; ++k) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int q = (int)__builtin_rintf(v[4 * k + i] * id);
+      sum += q;
+      word |= (uint32_t)(q & 0xff) << (8 * i);
+    }
+    wq[k] = word;
+  }
+  if constexpr (CL == 1) sum += dpp_i<0xB1>(sum);
+#pragma unroll
+  for (int k = 0; k < NV / 4; k += 4)
+    *reinterpret_cast<u32x4*>(xw + lane * (NV / 4) + k) = u32x4{wq[k], wq[k + 1], wq[k + 2], wq[k + 3]};
+  const int blk = CL == 1 ? lane >> 1 : lane;
+  if (CL == 2 || (lane & 1) == 0) {
+    xw[CL * 256 + blk] = __float_as_uint(d);
+    xw[CL * 288 + blk] = (uint32_t)sum;
+  }
+}
+
+template <int CL, int NB, int T, int MODE, bool DUMP, bool QIN, bool QOUT>
+__global__ void __launch_bounds__(QOUT ? 640 : 1024) gemv_dot4_kernel(Dot4Args a) {
   constexpr int RB = 4 * T;  // virtual rows per workgroup (4 per step)
   __shared__ float red[NB][kMaxWaves * CL][RB];
+  constexpr int kXW = CL * 320;  // QIN: LDS words per wave (q, d, s of its K range)
+  __shared__ uint32_t xq[QIN ? kMaxWaves * kXW : 1];
 
   const int lane = threadIdx.x & 63;
   const int w = threadIdx.x >> 6;
@@ -99,6 +178,10 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
   // ---- stream the rows ----
   float acc[T][NB][CL];  // one partial per 1024-column slice
 
+  float4 xv[QIN ? 4 * CL : 1];
+  if constexpr (QIN) load_lane_x<CL>(a.x + (size_t)a.m0 * a.ldx, w * CL * 1024 + lane * 16 * CL, K, xv);
+  __builtin_amdgcn_sched_barrier(0);
+
   // Issue every code and scale load of the workgroup's rows first (the HBM
   // stream), then the activation (L2-resident). The scheduling barriers keep
   // the compiler from hoisting consumers of early loads above later issues,
@@ -125,6 +208,12 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
 
   __builtin_amdgcn_sched_barrier(0);
 
+  if constexpr (QIN) {
+    quantize_lane<CL>(xv, w * CL * 1024 + lane * 16 * CL < K, lane, &xq[w * kXW]);
+    // LDS only: the weight loads stay in flight
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+  }
+
   // ---- activation registers ----
   uint32_t aq[NB][CL][16];
   float ad[NB][CL][2];
@@ -135,7 +224,9 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
     for (int j = 0; j < CL; ++j) {
       if (cval[j] && b < a.nb) {
         const size_t m = (size_t)(a.m0 + b);
-        const uint4* qp = reinterpret_cast<const uint4*>(a.q + m * K + (size_t)chunk[j] * 64);
+        const int lc = j * 16 + l16;  // QIN: chunk within the wave's LDS region
+        const uint4* qp = QIN ? reinterpret_cast<const uint4*>(&xq[w * kXW + lc * 16])
+                              : reinterpret_cast<const uint4*>(a.q + m * K + (size_t)chunk[j] * 64);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const uint4 v = qp[i];
@@ -144,8 +235,10 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
           aq[b][j][4 * i + 2] = v.z;
           aq[b][j][4 * i + 3] = v.w;
         }
-        const float2 dv = *reinterpret_cast<const float2*>(a.d + m * nsub + 2 * chunk[j]);
-        const int2 sv = *reinterpret_cast<const int2*>(a.s + m * nsub + 2 * chunk[j]);
+        const float2 dv = QIN ? *reinterpret_cast<const float2*>(&xq[w * kXW + CL * 256 + 2 * lc])
+                              : *reinterpret_cast<const float2*>(a.d + m * nsub + 2 * chunk[j]);
+        const int2 sv = QIN ? *reinterpret_cast<const int2*>(&xq[w * kXW + CL * 288 + 2 * lc])
+                            : *reinterpret_cast<const int2*>(a.s + m * nsub + 2 * chunk[j]);
         ad[b][j][0] = dv.x * 0.0625f;  // exact: the dot returns 16 * I
         ad[b][j][1] = dv.y * 0.0625f;
         an[b][j][0] = -sv.x;
@@ -202,6 +295,49 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
   const int nsl = nw * CL;  // slices; those past the row end hold +0
 
   // ---- epilogue: fixed-order sum over waves ----
+  if constexpr (QOUT) {
+    // One 32-row block per activation row: lane r of half-wave b computes
+    // row r0 + r, then the half-wave quantizes the block (every lane takes
+    // part in the DPP reductions; dead halves work on zeros).
+    static_assert(MODE == BTF_GEMV_SWIGLU ? 2 * T == 32 : RB == 32, "QOUT: one 32-row block per workgroup");
+    for (int i0 = 0; i0 < NB * 32; i0 += blockDim.x) {
+      const int t = i0 + threadIdx.x;
+      const int b = t >> 5, r = t & 31;
+      const bool live = t < NB * 32 && b < a.nb;  // uniform over the half-wave
+      const size_t m = (size_t)(a.m0 + (live ? b : 0));
+      const int row = r0 + r;  // N % 32 == 0: the block is inside the output
+      float v = 0.f;
+      if (live) {
+        if constexpr (MODE == BTF_GEMV_SWIGLU) {
+          float g = 0.f, u = 0.f;
+          for (int k = 0; k < nsl; ++k) {
+            g += red[b][k][2 * r];
+            u += red[b][k][2 * r + 1];
+          }
+          v = g / (1.0f + expf(-g)) * u;
+        } else {
+          float sum = 0.f;
+          for (int k = 0; k < nsl; ++k) sum += red[b][k][r];
+          v = MODE == BTF_GEMV_ADD ? y[m * ldy + row] + sum : sum;
+        }
+        y[m * ldy + row] = v;
+      }
+      float dq;
+      int sq;
+      const int q = q8_half(v, dq, sq);
+      uint32_t wq = (uint32_t)(q & 0xff) << (8 * (r & 3));
+      wq |= (uint32_t)dpp_i<0xB1>((int)wq);  // quad_perm(1,0,3,2)
+      wq |= (uint32_t)dpp_i<0x4E>((int)wq);  // quad_perm(2,3,0,1)
+      if (live) {
+        if ((r & 3) == 0) *reinterpret_cast<uint32_t*>(a.oq + m * N + row) = wq;
+        if (r == 0) {
+          a.od[m * (N / 32) + r0 / 32] = dq;
+          a.os[m * (N / 32) + r0 / 32] = sq;
+        }
+      }
+    }
+    return;
+  }
   for (int i = threadIdx.x; i < NB * RB; i += blockDim.x) {
     const int b = i / RB;
     const int v = i - b * RB;
@@ -230,19 +366,46 @@ __global__ void __launch_bounds__(1024) gemv_dot4_kernel(Dot4Args a) {
   }
 }
 
-template <int CL, int NB, int T, int MODE, bool DUMP>
+template <int CL, int NB, int T, int MODE, bool DUMP, bool QIN = false, bool QOUT = false>
 void launch_one(const Dot4Args& a, int grid, int threads, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_dot4_kernel<CL, NB, T, MODE, DUMP>), dim3(grid), dim3(threads), 0, st, a);
+  hipLaunchKernelGGL((gemv_dot4_kernel<CL, NB, T, MODE, DUMP, QIN, QOUT>), dim3(grid), dim3(threads), 0, st, a);
 }
 
-template <int CL, int NB, int T, bool DUMP>
+template <int CL, int NB, int T, bool DUMP, bool QIN = false>
 void by_mode(int mode, const Dot4Args& a, int grid, int threads, hipStream_t st) {
   if (mode == BTF_GEMV_STORE)
-    launch_one<CL, NB, T, BTF_GEMV_STORE, DUMP>(a, grid, threads, st);
+    launch_one<CL, NB, T, BTF_GEMV_STORE, DUMP, QIN>(a, grid, threads, st);
   else if (mode == BTF_GEMV_ADD)
-    launch_one<CL, NB, T, BTF_GEMV_ADD, DUMP>(a, grid, threads, st);
+    launch_one<CL, NB, T, BTF_GEMV_ADD, DUMP, QIN>(a, grid, threads, st);
   else
-    launch_one<CL, NB, T, BTF_GEMV_SWIGLU, DUMP>(a, grid, threads, st);
+    launch_one<CL, NB, T, BTF_GEMV_SWIGLU, DUMP, QIN>(a, grid, threads, st);
+}
+
+// QIN (one activation row): CL 1 with T 2/4/8, CL 2 with T 2/4.
+template <int CL>
+void qin_by_t(int T, int mode, const Dot4Args& a, int grid, int threads, hipStream_t st) {
+  if (T == 2) {
+    by_mode<CL, 1, 2, false, true>(mode, a, grid, threads, st);
+  } else if constexpr (CL == 2) {
+    by_mode<CL, 1, 4, false, true>(mode, a, grid, threads, st);
+  } else {
+    if (T == 4)
+      by_mode<CL, 1, 4, false, true>(mode, a, grid, threads, st);
+    else
+      by_mode<CL, 1, 8, false, true>(mode, a, grid, threads, st);
+  }
+}
+
+// QOUT (one activation row, with or without QIN): T = 8 (swiglu 16, CL 1
+// only: with 2 chunks per lane it would not fit the register file).
+template <int CL, bool QIN>
+void qout_by_mode(int mode, const Dot4Args& a, int grid, int threads, hipStream_t st) {
+  if (mode == BTF_GEMV_STORE)
+    launch_one<CL, 1, 8, BTF_GEMV_STORE, false, QIN, true>(a, grid, threads, st);
+  else if (mode == BTF_GEMV_ADD)
+    launch_one<CL, 1, 8, BTF_GEMV_ADD, false, QIN, true>(a, grid, threads, st);
+  else if constexpr (CL == 1)
+    launch_one<CL, 1, 16, BTF_GEMV_SWIGLU, false, QIN, true>(a, grid, threads, st);
 }
 
 // Instantiated shapes: CL=1 with NB 1/2 (T 2/4/8) and NB 4 (T 2); CL=2 with
@@ -272,14 +435,19 @@ void by_t(int T, int mode, bool dump, const Dot4Args& a, int grid, int threads, 
 }  // namespace
 
 int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& act, int mode, int32_t* dump,
-              hipStream_t st, const DevState& ds) {
+              hipStream_t st, const DevState& ds, const float* x, int ldx, const Q8* qout) {
   const int cpr = K / 64;
   // chunks per lane: 1 up to K = 16384 (16 waves x 16 lanes x 64 columns), else 2
-  const int CL = cpr <= 16 * kMaxWaves ? 1 : 2;
+  // (the fused output quantize runs at most 10 waves: 2 chunks per lane past K = 10240)
+  const int CL = cpr <= (qout ? 160 : 16 * kMaxWaves) ? 1 : 2;
   const int nw = (cpr + 16 * CL - 1) / (16 * CL);
   if (nw > kMaxWaves) return fail(BTF_ERR_ARGS, "gemv: K too large for the dot4 path");
   const int NB = nb <= 1 ? 1 : nb <= 2 ? 2 : 4;
   if (CL * NB > 4 || (CL == 2 && NB > 1)) return fail(BTF_ERR_ARGS, "gemv: batch too large for the dot4 path");
+  if ((x || qout) && (nb != 1 || dump)) return fail(BTF_ERR_ARGS, "gemv: the fused quantizes take one row");
+  if (qout && nw > 10) return fail(BTF_ERR_ARGS, "gemv: the fused output quantize takes K <= 20480");
+  if (qout && CL == 2 && mode == BTF_GEMV_SWIGLU)
+    return fail(BTF_ERR_ARGS, "gemv: the fused output quantize takes swiglu with K <= 10240");
 
   // rows per workgroup: 4*T (swiglu: 2*T output rows); keep >= 2 workgroups per CU
   const int unit = mode == BTF_GEMV_SWIGLU ? 2 : 4;
@@ -290,6 +458,7 @@ int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   if (NB * CL >= 4 && T > 2) T = 2;  // register budget
   if (CL == 2 && T > 4) T = 4;
   if (dump) T = 2;
+  if (qout) T = mode == BTF_GEMV_SWIGLU ? 16 : 8;  // one 32-row output block per workgroup
 
   Dot4Args a{};
   int wg = 0;
@@ -320,9 +489,30 @@ int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   a.m0 = m0;
   a.nb = nb;
   a.dump = dump;
+  a.x = x;
+  a.ldx = ldx;
+  if (qout) {
+    a.oq = const_cast<int8_t*>(qout->q);
+    a.od = const_cast<float*>(qout->d);
+    a.os = const_cast<int32_t*>(qout->s);
+  }
   if (wg == 0) return BTF_OK;
   const int threads = 64 * nw;
   const bool dmp = dump != nullptr;
+  if (qout) {
+    if (CL == 1)
+      x ? qout_by_mode<1, true>(mode, a, wg, threads, st) : qout_by_mode<1, false>(mode, a, wg, threads, st);
+    else
+      x ? qout_by_mode<2, true>(mode, a, wg, threads, st) : qout_by_mode<2, false>(mode, a, wg, threads, st);
+    return launch_status("gemv_dot4_kernel");
+  }
+  if (x) {
+    if (CL == 1)
+      qin_by_t<1>(T, mode, a, wg, threads, st);
+    else
+      qin_by_t<2>(T, mode, a, wg, threads, st);
+    return launch_status("gemv_dot4_kernel");
+  }
   if (CL == 1) {
     if (NB == 1) by_t<1, 1>(T, mode, dmp, a, wg, threads, st);
     else if (NB == 2) by_t<1, 2>(T, mode, dmp, a, wg, threads, st);

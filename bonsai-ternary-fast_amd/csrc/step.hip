@@ -602,38 +602,6 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
 }
 
 // ---------------------------------------------------------------- I/O waves
-// Q8 of 32 values held by a 32-lane half-wave (lane j holds value j), identical
-// to the q8 kernel / include/btf/packed.hpp:117-134. Returns q of this lane;
-// d and s valid in every lane of the half.
-// The reductions run in DPP within 16-lane rows, then v_permlane16_swap
-// combines rows 0/1 and 2/3 (no LDS traffic).
-__device__ __forceinline__ float half32_max(float v) {
-  v = fmaxf(v, dpp_f<0xB1>(v));
-  v = fmaxf(v, dpp_f<0x4E>(v));
-  v = fmaxf(v, dpp_f<0x141>(v));
-  v = fmaxf(v, dpp_f<0x140>(v));
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ int half32_sum(int v) {
-  v += dpp_i<0xB1>(v);
-  v += dpp_i<0x4E>(v);
-  v += dpp_i<0x141>(v);
-  v += dpp_i<0x140>(v);
-  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
-  return (int)r[0] + (int)r[1];
-}
-__device__ __forceinline__ int q8_half(float v, float& d, int& s) {
-  const float amax = half32_max(fabsf(v));
-  float dd = h2f(f2h_bits(amax / 127.0f));
-  if (amax == 0.f) dd = copysignf(0.f, __shfl(v, 31, 32));  // all 32 lanes of the half take this branch
-  d = dd;
-  const float id = amax != 0.f ? 127.0f / amax : 0.f;
-  const int q = (int)__builtin_rintf(v * id);
-  s = half32_sum(q);
-  return q;
-}
-
 // Publish one 32-value unit held by a half-wave: fp32 LL words, plain output
 // and the Q8 LL words.
 __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, float v, bool valid, uint32_t tag) {

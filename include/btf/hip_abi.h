@@ -110,6 +110,22 @@ const char* btf_hip_last_error(void);
 int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q8act* a, int32_t* I_out,
                           btf_stream_t stream);
 
+/* launch_gemv with the Q8_0 quantizes of a GEMV chain fused in (the v_dot4
+ * kernel, one launch per activation row):
+ *  - input: exactly one of `a` (Q8 rows, as launch_gemv) or `x` (fp32 rows
+ *    [M][ldx], quantized inside the launch with launch_prep's arithmetic, no
+ *    norm or transform; x 16-byte aligned, ldx >= K, ldx % 4 == 0);
+ *  - out (optional): the Q8 of the output rows (segment 0's y after the
+ *    add / swiglu), written as launch_prep would write them for the next
+ *    GEMV (q [M][N], d and s [M][N/32]); one output segment, N % 32 == 0,
+ *    K <= 20480 (swiglu K <= 10240).
+ * The results (y, and the Q8 rows) are bit-identical to launch_prep +
+ * launch_gemv on the v_dot4 path. No reference counterpart: the reference
+ * decoder launches the quantize and the GEMV separately
+ * (src/cuda/gpu_decoder.cu:411-418). */
+int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, const float* x,
+                           int ldx, int mode, const btf_q8act* out, btf_stream_t stream);
+
 /* GEMV path policy: batches of M >= mfma_min_m rows run on the int8-MFMA
  * kernel, smaller ones on the v_dot4 kernel. 0 restores the default.
  * Process-global; for tests and benchmarks. Returns the previous value. */

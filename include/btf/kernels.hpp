@@ -80,6 +80,22 @@ inline void launch_gemv(const GemvSeg* segs, int nseg, int K, int M, const Q8Act
   detail::check(btf_hip_launch_gemv(s, nseg, K, M, &q, mode, st), "launch_gemv");
 }
 
+// launch_gemv with the chain's quantizes fused in (no counterpart in
+// kernels.cuh: the decoder's launch_prep + launch_gemv pairs without norm or
+// transform, src/cuda/gpu_decoder.cu:411-418): input from Q8 rows `a` or fp32
+// rows `x`; `out` (optional) receives the Q8 rows of the output.
+inline void launch_gemv_ex(const GemvSeg* segs, int nseg, int K, int M, const Q8Act* a, const float* x, int ldx,
+                           GemvMode mode, const Q8Act* out, btf_stream_t st) {
+  if (nseg < 1 || nseg > 3) throw std::runtime_error("launch_gemv_ex: gemv: 1..3 segments");
+  btf_gemv_seg s[3] = {};
+  for (int i = 0; i < nseg; ++i) s[i] = btf_gemv_seg{segs[i].codes, segs[i].scales, segs[i].N, segs[i].y, segs[i].ldy};
+  btf_q8act qa{}, qo{};
+  if (a) qa = btf_q8act{a->q, a->d, reinterpret_cast<int32_t*>(a->s)};
+  if (out) qo = btf_q8act{out->q, out->d, reinterpret_cast<int32_t*>(out->s)};
+  detail::check(btf_hip_launch_gemv_ex(s, nseg, K, M, a ? &qa : nullptr, x, ldx, mode, out ? &qo : nullptr, st),
+                "launch_gemv_ex");
+}
+
 // ---- the decode-step program (no counterpart in kernels.cuh: it replaces
 // the per-step graph of GEMV launches, src/cuda/gpu_decoder.cu:452-486)
 class StepProgram {

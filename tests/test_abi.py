@@ -81,6 +81,21 @@ def test_invalid_arguments_rejected_on_host():
     assert h.launch_repack_raw(codes, 10, codes + 8, scales) == ARGS                 # codes alignment
     assert h.launch_prep_raw(y, 100, 1, 100, None, 0.0, None, None, 0, act) == ARGS   # n % 32
     assert h.launch_prep_raw(y, 64, 1, 128, None, 0.0, None, None, 0, act) == ARGS    # ldx < n
+    # fused-quantize GEMV: one input, x alignment / stride, K, the output's shape, and the launch_gemv checks
+    xa = 0x700000
+    ex = h.launch_gemv_ex_raw
+    assert ex([seg], 1, 1024, 1, None, xa + 4, 1024, 0) == ARGS                # x alignment
+    assert ex([seg], 1, 1024, 1, None, xa, 1000, 0) == ARGS                    # ldx < K
+    assert ex([seg], 1, 1024, 1, None, xa, 1026, 0) == ARGS                    # ldx % 4
+    assert ex([seg], 1, 1000, 1, None, xa, 1024, 0) == ARGS                    # K % 128
+    assert ex([seg], 1, 40960, 1, None, xa, 40960, 0) == ARGS                  # K too large
+    assert ex([seg], 1, 1024, 1, None, None, 1024, 0) == ARGS                  # no input
+    assert ex([seg], 1, 1024, 1, act, xa, 1024, 0) == ARGS                     # two inputs
+    assert ex([seg], 1, 1024, 1, None, xa, 1024, 2) == ARGS                    # swiglu needs 2 segs
+    assert ex([h.GemvSeg(codes, scales, 48, y, 48)], 1, 1024, 1, act, None, 0, 0, act) == ARGS  # out: N % 32
+    assert ex([seg, seg], 2, 1024, 1, act, None, 0, 0, act) == ARGS            # out: one segment
+    assert ex([seg], 1, 1024, 1, act, None, 0, 0, h.Q8Act(0x400001, 0x500000, 0x600000)) == ARGS  # out align
+    assert ex([seg], 1, 1024, 0, None, xa, 1024, 0) == h.BTF_OK                # M = 0: no-op
     # step programs: every structural error is caught before the device is touched
     G = h.GemvMode
     vecs = [h.StepVec(1024, y), h.StepVec(1024, None)]

@@ -311,6 +311,132 @@ def test_prep_then_gemv_end_to_end(hip, oracle):
     assert_close_1e3(host(y), ref, "prep+gemv")
 
 
+@pytest.mark.parametrize("K,M", [(1024, 1), (5120, 1), (5120, 3), (17408, 1), (20480, 2)])
+def test_gemv_fused_input_quantize(hip, oracle, K, M):
+    """launch_gemv_ex from fp32 rows (the Q8 quantize inside the GEMV launch)
+    equals launch_prep + launch_gemv (v_dot4 path) bit for bit in every mode,
+    and the emulator's quantize + GEMV to the float bar; inputs include the
+    quantizer's edge rows (zero blocks with +-0 ends, ties, subnormal d) and
+    ldx > K."""
+    rng = np.random.default_rng(777 + K + M)
+    N = 96
+    x = (rng.standard_normal((M, K)) * 3).astype(np.float32)
+    x[0, :] = _special_rows(K)[M % 6] if M > 1 else x[0, :]
+    if M == 1:
+        x[0, :128] = _special_rows(K)[0, :128]
+    ldx = K + 4
+    xp = np.zeros((M, ldx), np.float32)
+    xp[:, :K] = x
+    xd = dev(xp)
+    q, d, s = oracle.quantize_rows(x)
+    gate, up, mat = (random_mat(oracle, rng, N, K) for _ in range(3))
+    torch = _torch()
+    a = hip.Q8Act(zeros((M, K), torch.int8), zeros((M, K // 32), torch.float32), zeros((M, K // 32), torch.int32))
+    hip.launch_prep(xd, ldx, M, K, None, 0.0, None, None, 0, a, stream())
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    for mode in (hip.GemvMode.kStore, hip.GemvMode.kAdd, hip.GemvMode.kSwiglu):
+        outs = []
+        for fused in (False, True):
+            y = dev(y0.copy())
+            if mode == hip.GemvMode.kSwiglu:
+                segs = [hip.GemvSeg(dev(gate[0]), dev(gate[1]), N, y, N), hip.GemvSeg(dev(up[0]), dev(up[1]), N, None, 0)]
+            else:
+                segs = [hip.GemvSeg(dev(mat[0]), dev(mat[1]), N, y, N)]
+            if fused:
+                hip.launch_gemv_ex(segs, K, M, x=xd, ldx=ldx, mode=mode, stream=stream())
+            else:  # on the v_dot4 path too (M >= 3 would take the MFMA kernel, another float order)
+                prev = hip.gemv_set_policy(1 << 20)
+                try:
+                    hip.launch_gemv(segs, K, M, a, mode, stream())
+                finally:
+                    hip.gemv_set_policy(prev)
+            outs.append(host(y))
+        assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), f"mode {mode}"
+        if mode == hip.GemvMode.kSwiglu:
+            ref = oracle.swiglu(oracle.gemv(gate[0], gate[1], K, q, d, s), oracle.gemv(up[0], up[1], K, q, d, s))
+        else:
+            ref = oracle.gemv(mat[0], mat[1], K, q, d, s, y=y0.copy(), add=mode == hip.GemvMode.kAdd)
+        assert_close_1e3(outs[1], ref, f"fused mode {mode}")
+
+
+@pytest.mark.parametrize("K,N,M,xin", [(1024, 64, 1, False), (5120, 160, 2, False), (5120, 96, 1, True),
+                                       (17408, 64, 1, False), (20480, 32, 1, True)])
+def test_gemv_fused_output_quantize(hip, oracle, K, N, M, xin):
+    """launch_gemv_ex with a Q8 output: y equals launch_gemv's (v_dot4 path)
+    bit for bit and the Q8 rows equal launch_prep of that y (and the
+    oracle's quantize) bit for bit, in every mode (swiglu only where
+    K <= 10240), from Q8 or fp32 input."""
+    rng = np.random.default_rng(99 + K + N + M)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    xd = dev(x)
+    q, d, s = oracle.quantize_rows(x)
+    torch = _torch()
+    a = q8_dev(q, d, s, hip)
+    mat, gate, up = (random_mat(oracle, rng, N, K) for _ in range(3))
+    mat[0][:32] = 0x55  # rows 0..31 all trit 0: an all-zero output block (store; add onto zeros)
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    y0[:, :32] = 0.0
+    modes = [hip.GemvMode.kStore, hip.GemvMode.kAdd] + ([hip.GemvMode.kSwiglu] if K <= 10240 else [])
+    for mode in modes:
+        if mode == hip.GemvMode.kSwiglu:
+            mk = lambda y: [hip.GemvSeg(dev(gate[0]), dev(gate[1]), N, y, N),
+                            hip.GemvSeg(dev(up[0]), dev(up[1]), N, None, 0)]
+        else:
+            mk = lambda y: [hip.GemvSeg(dev(mat[0]), dev(mat[1]), N, y, N)]
+        y_ref = dev(y0.copy())
+        prev = hip.gemv_set_policy(1 << 20)
+        try:
+            hip.launch_gemv(mk(y_ref), K, M, a, mode, stream())
+        finally:
+            hip.gemv_set_policy(prev)
+        y = dev(y0.copy())
+        out = hip.Q8Act(zeros((M, N), torch.int8), zeros((M, N // 32), torch.float32), zeros((M, N // 32), torch.int32))
+        if xin:
+            hip.launch_gemv_ex(mk(y), K, M, x=xd, ldx=K, mode=mode, out=out, stream=stream())
+        else:
+            hip.launch_gemv_ex(mk(y), K, M, a=a, mode=mode, out=out, stream=stream())
+        yh = host(y)
+        assert np.array_equal(yh.view(np.uint32), host(y_ref).view(np.uint32)), f"y, mode {mode}"
+        rq, rd, rs = oracle.quantize_rows(yh)
+        assert np.array_equal(host(out.q), rq), f"q, mode {mode}"
+        assert np.array_equal(host(out.d).view(np.uint32), rd.view(np.uint32)), f"d, mode {mode}"
+        assert np.array_equal(host(out.s), rs), f"s, mode {mode}"
+
+
+def test_gemv_fused_chain_matches_prep_chain(hip, oracle):
+    """A 3-GEMV chain whose quantizes ride in the GEMV launches (fp32 input
+    quantized by the first, Q8 outputs feeding the next) equals the chain of
+    launch_prep + launch_gemv pairs bit for bit."""
+    rng = np.random.default_rng(4242)
+    K0, K1, K2 = 5120, 2048, 1024
+    m0, m1, m2 = random_mat(oracle, rng, K1, K0), random_mat(oracle, rng, K2, K1), random_mat(oracle, rng, 96, K2)
+    x = rng.standard_normal((1, K0)).astype(np.float32)
+    torch = _torch()
+    def q8(n):
+        return hip.Q8Act(zeros((1, n), torch.int8), zeros((1, n // 32), torch.float32), zeros((1, n // 32), torch.int32))
+    res = []
+    for fused in (False, True):
+        xd = dev(x)
+        y1, y2, y3 = zeros((1, K1), torch.float32), zeros((1, K2), torch.float32), zeros((1, 96), torch.float32)
+        a1, a2 = q8(K1), q8(K2)
+        if fused:
+            hip.launch_gemv_ex([hip.GemvSeg(dev(m0[0]), dev(m0[1]), K1, y1, K1)], K0, 1, x=xd, ldx=K0, out=a1,
+                               stream=stream())
+            hip.launch_gemv_ex([hip.GemvSeg(dev(m1[0]), dev(m1[1]), K2, y2, K2)], K1, 1, a=a1, out=a2, stream=stream())
+            hip.launch_gemv([hip.GemvSeg(dev(m2[0]), dev(m2[1]), 96, y3, 96)], K2, 1, a2, hip.GemvMode.kStore, stream())
+        else:
+            a0 = q8(K0)
+            hip.launch_prep(xd, K0, 1, K0, None, 0.0, None, None, 0, a0, stream())
+            hip.launch_gemv([hip.GemvSeg(dev(m0[0]), dev(m0[1]), K1, y1, K1)], K0, 1, a0, hip.GemvMode.kStore, stream())
+            hip.launch_prep(y1, K1, 1, K1, None, 0.0, None, None, 0, a1, stream())
+            hip.launch_gemv([hip.GemvSeg(dev(m1[0]), dev(m1[1]), K2, y2, K2)], K1, 1, a1, hip.GemvMode.kStore, stream())
+            hip.launch_prep(y2, K2, 1, K2, None, 0.0, None, None, 0, a2, stream())
+            hip.launch_gemv([hip.GemvSeg(dev(m2[0]), dev(m2[1]), 96, y3, 96)], K2, 1, a2, hip.GemvMode.kStore, stream())
+        res.append([host(t) for t in (y1, y2, y3)])
+    for u, v in zip(*res):
+        assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+
+
 def test_graph_replay_matches_eager(hip, oracle):
     """A captured quantize + GEMV + add sequence replays identically (several
     replays with eager work and syncs between them)."""
