@@ -178,14 +178,36 @@ __global__ void __launch_bounds__(QOUT ? 640 : 1024) gemv_dot4_kernel(Dot4Args a
   // ---- stream the rows ----
   float acc[T][NB][CL];  // one partial per 1024-column slice
 
+  // The activation (L2-resident) is loaded first, then every code and scale
+  // load of the workgroup's rows (the HBM stream): loads return in order, so
+  // the dot products of row step t start as soon as its codes are in, while
+  // the later steps stream. The scheduling barriers keep the compiler from
+  // hoisting consumers of early loads above later issues, which would
+  // serialise the round trips. Lanes past the row end or batch load valid
+  // addresses and are zeroed after the barrier.
   float4 xv[QIN ? 4 * CL : 1];
-  if constexpr (QIN) load_lane_x<CL>(a.x + (size_t)a.m0 * a.ldx, w * CL * 1024 + lane * 16 * CL, K, xv);
+  uint4 rq[QIN ? 1 : NB][CL][4];
+  float2 rd[QIN ? 1 : NB][CL];
+  int2 rs[QIN ? 1 : NB][CL];
+  if constexpr (QIN) {
+    load_lane_x<CL>(a.x + (size_t)a.m0 * a.ldx, w * CL * 1024 + lane * 16 * CL, K, xv);
+  } else {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+#pragma unroll
+      for (int j = 0; j < CL; ++j) {
+        const size_t m = (size_t)(a.m0 + (b < a.nb ? b : 0));
+        const int c = cval[j] ? chunk[j] : 0;
+        const uint4* qp = reinterpret_cast<const uint4*>(a.q + m * K + (size_t)c * 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) rq[b][j][i] = qp[i];
+        rd[b][j] = *reinterpret_cast<const float2*>(a.d + m * nsub + 2 * c);
+        rs[b][j] = *reinterpret_cast<const int2*>(a.s + m * nsub + 2 * c);
+      }
+    }
+  }
   __builtin_amdgcn_sched_barrier(0);
 
-  // Issue every code and scale load of the workgroup's rows first (the HBM
-  // stream), then the activation (L2-resident). The scheduling barriers keep
-  // the compiler from hoisting consumers of early loads above later issues,
-  // which would serialise the round trips.
   u32x4 wv[T][CL];
   uint32_t sc[T][CL];  // 32-bit: keeps every scale load in its own register
   int rowv[T];
@@ -223,22 +245,17 @@ __global__ void __launch_bounds__(QOUT ? 640 : 1024) gemv_dot4_kernel(Dot4Args a
 #pragma unroll
     for (int j = 0; j < CL; ++j) {
       if (cval[j] && b < a.nb) {
-        const size_t m = (size_t)(a.m0 + b);
         const int lc = j * 16 + l16;  // QIN: chunk within the wave's LDS region
-        const uint4* qp = QIN ? reinterpret_cast<const uint4*>(&xq[w * kXW + lc * 16])
-                              : reinterpret_cast<const uint4*>(a.q + m * K + (size_t)chunk[j] * 64);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const uint4 v = qp[i];
+          const uint4 v = QIN ? reinterpret_cast<const uint4*>(&xq[w * kXW + lc * 16])[i] : rq[QIN ? 0 : b][j][i];
           aq[b][j][4 * i + 0] = v.x;
           aq[b][j][4 * i + 1] = v.y;
           aq[b][j][4 * i + 2] = v.z;
           aq[b][j][4 * i + 3] = v.w;
         }
-        const float2 dv = QIN ? *reinterpret_cast<const float2*>(&xq[w * kXW + CL * 256 + 2 * lc])
-                              : *reinterpret_cast<const float2*>(a.d + m * nsub + 2 * chunk[j]);
-        const int2 sv = QIN ? *reinterpret_cast<const int2*>(&xq[w * kXW + CL * 288 + 2 * lc])
-                            : *reinterpret_cast<const int2*>(a.s + m * nsub + 2 * chunk[j]);
+        const float2 dv = QIN ? *reinterpret_cast<const float2*>(&xq[w * kXW + CL * 256 + 2 * lc]) : rd[QIN ? 0 : b][j];
+        const int2 sv = QIN ? *reinterpret_cast<const int2*>(&xq[w * kXW + CL * 288 + 2 * lc]) : rs[QIN ? 0 : b][j];
         ad[b][j][0] = dv.x * 0.0625f;  // exact: the dot returns 16 * I
         ad[b][j][1] = dv.y * 0.0625f;
         an[b][j][0] = -sv.x;

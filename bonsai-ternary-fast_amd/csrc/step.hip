@@ -738,8 +738,14 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
 
   if (wave < kCW)
     compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
-  else
+  else {
+    // The I/O waves' epilogue of an op is on the chain's critical path while
+    // the compute waves already run the next op's dot products on the same
+    // SIMDs: their instructions issue first (the waits in between sleep).
+    __builtin_amdgcn_s_setprio(3);
     io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
+    __builtin_amdgcn_s_setprio(0);
+  }
 
   // ---------------- end of step: count the workgroup out; the last one to
   // arrive advances the epoch for the next launch (it is read before any
