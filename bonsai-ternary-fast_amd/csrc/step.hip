@@ -1,17 +1,17 @@
 // step.hip -- a whole batch-1 decode step's chain of ternary GEMVs in ONE
 // persistent kernel launch (gfx950).
 //
-// Why: in a stream or hipGraph every kernel boundary costs ~4-5 us on MI355X
-// (release/acquire of the per-XCD L2s plus dispatch), while a 27B-layer GEMV
-// moves 7-47 MB (1-7 us at HBM speed). The reference decoder captures a step
+// Why: in a stream or hipGraph a dependent kernel costs ~2 us of launch plus
+// its ramp and drain on MI355X, while a 27B-layer GEMV moves 7-47 MB (1-7 us
+// at HBM speed). The reference decoder captures a step
 // as one CUDA graph of ~514 launches (src/cuda/gpu_decoder.cu:452-486); here
 // the same GEMV chain (with the Q8 quantize of every GEMV input) is one launch.
 //
 // Execution model (one workgroup per CU, all co-resident: cooperative launch):
 //  * Ops run in program order. Output rows of every op are owned in 32-row
 //    units (one Q8 block of the output), spread round-robin over workgroups
-//    with a rotation that continues from op to op so each workgroup's total
-//    work over the step is balanced.
+//    with a rotation chosen op by op to keep each workgroup's total work over
+//    the step balanced.
 //  * Cross-workgroup data moves through "LL" words: 8 bytes = 4 data bytes +
 //    a 32-bit version tag, written and read with agent-scope relaxed atomics
 //    (write-through / read-through the per-XCD L2s). A consumer polls the
@@ -23,13 +23,14 @@
 //  * Inside a workgroup: 10 compute waves stream the weights. Each keeps
 //    kRing items (16-byte code chunks per lane) in flight in registers, and
 //    the refills of an op's last batch load the NEXT op's first items, so
-//    the ring never drains between ops. Between two ops the compute waves
-//    (640 lanes) fetch the next op's input into LDS in one round of LL loads
-//    (and, for add mode, the old values of the workgroup's rows), while the
-//    2 I/O waves reduce the previous op's partial sums, apply its epilogue
-//    and publish its outputs. Intra-workgroup hand-offs use s_barrier
-//    without a memory fence (LDS only), so the weight stream stays in flight
-//    across them.
+//    the ring never drains between ops. Items run unit by unit; each compute
+//    wave fetches (polls) only the input slices its own items read, so it
+//    starts as soon as those are published. The 2 I/O waves publish each unit
+//    as soon as the compute waves' per-unit counts say it is complete, and
+//    fetch the input of an "early" op (one whose producers are two or more
+//    ops back) while the previous op computes. One s_barrier per op (without
+//    a memory fence: LDS only) separates ops, so the weight stream stays in
+//    flight across it.
 //  * Op descriptors are staged in LDS at launch.
 //  * The dot products, the 16-lane DPP reduction and the fixed-order sum over
 //    1024-column slices are those of gemv_dot4_kernel, so outputs are
@@ -58,7 +59,8 @@ constexpr int kRing = 8;                    // weight items (16 B per lane) in f
 constexpr int kMaxK = 20480;                // widest GEMV input
 constexpr int kMaxPart = 8192;              // partial sums per op per workgroup
 constexpr int kMaxOps = 384;                // ops per program (descriptors live in LDS)
-constexpr int kMaxOld = 1024;               // rows per workgroup of an add-mode op (old values in LDS)
+constexpr int kMaxOld = 1024;               // rows per workgroup of an add-mode op (the LDS carry)
+constexpr int kMaxUnits = 256;              // units of one op per workgroup (kMaxPart / 32)
 constexpr int kWordsPerBlock = 10;          // LL words per 32-value Q8 block
 constexpr int kSlots = 3;                   // LL buffers of each kind per vector (versions in turn)
 constexpr uint32_t kSpinMax = 1u << 20;     // poll bound (each poll is a memory round trip: ~1 s)
@@ -123,9 +125,10 @@ struct Lds {
   uint32_t act_q[2][kMaxK / 4];  // q bytes of an op's input (by op parity)
   float act_d[2][kMaxK / 32];    // d
   int32_t act_s[2][kMaxK / 32];  // s
-  float part[kMaxPart];       // [local row][1024-column slice]
-  float oldv[2][kMaxOld];     // add mode: previous values of the workgroup's rows (by op parity)
+  float part[kMaxPart];       // [1024-column slice][local row]
   float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
+  uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
+  uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
   uint32_t epoch;
   uint32_t abort_;
   uint32_t spin_max;
@@ -174,54 +177,40 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
   return true;
 }
 
-// Fetch an op's input (its Q8 LL words, tag = the input producer's) into
-// LDS buffer `ob` and, for add mode without carry, the previous values of
-// this workgroup's rows (tag = the previous writer's) into L.oldv[ob],
-// polling until every tag matches. NL lanes (lane id lid) take words
-// lid + k*NL in rounds of B words per lane. The old-value loads are issued
-// first and checked last, so their round trip overlaps the input's.
-template <int NL, int B>
-__device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ctl* ctl, uint32_t base_tag, int wg, int G,
-                                            int ob) {
-  constexpr int kOld = (kMaxOld + NL - 1) / NL;  // old values per lane
+// Fetch LL words [a0, a1) and [b0, b1) of an op's input (its Q8 words, tag = the input
+// producer's) into LDS buffer `ob`, by the 64 lanes of one compute wave in
+// rounds of kFB words per lane, polling until every tag matches. A slice
+// whose items two waves share is fetched by both: the same values land twice.
+constexpr int kFB = 10;
+__device__ __forceinline__ void fetch_words(const OpDev& op, Lds& L, int lane, Ctl* ctl, uint32_t base_tag, int ob,
+                                            int a0, int a1, int b0, int b1) {
   const uint64_t* in = sgpr_ptr(op.in_q8);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
-  const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
-  const uint64_t* old = sgpr_ptr(op.old_f32);
-  const uint32_t told = base_tag + sgpr(op.old_tag);
-  const int first = first_unit(sgpr(op.rot), wg, G);
-  const int nold =
-      (sgpr(op.mode) == BTF_GEMV_ADD && !sgpr(op.carry_in)) ? units_of(sgpr(op.units), first, G) * 32 : 0;
-  const int N = sgpr(op.N);
-  uint64_t vo[kOld];
+  const int na = a1 - a0, nw = na + (b1 - b0);  // word k < nw: a0 + k, or b0 + k - na
+  for (int k0 = 0; k0 < nw; k0 += kFB * 64) {
+    uint64_t v[kFB];
+    int at[kFB];
 #pragma unroll
-  for (int b = 0; b < kOld; ++b) {
-    const int k = lid + b * NL;
-    const int row = (first + (k >> 5) * G) * 32 + (k & 31);
-    vo[b] = (k < nold && row < N) ? ll_load(old + row) : ((uint64_t)told << 32);
-  }
-  for (int base = lid; base < nin; base += B * NL) {
-    uint64_t v[B];
-#pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int idx = base + b * NL;
-      v[b] = idx < nin ? ll_load(in + idx) : ((uint64_t)tin << 32);
+    for (int b = 0; b < kFB; ++b) {
+      const int k = k0 + b * 64 + lane;
+      at[b] = k < nw ? (k < na ? a0 + k : b0 + k - na) : -1;
+      v[b] = at[b] >= 0 ? ll_load(in + at[b]) : ((uint64_t)tin << 32);
     }
     uint32_t spins = 0;
     for (;;) {
       uint32_t pending = 0;
 #pragma unroll
-      for (int b = 0; b < B; ++b) pending |= ((uint32_t)(v[b] >> 32) != tin) ? (1u << b) : 0u;
-      if (pending == 0) break;
+      for (int b = 0; b < kFB; ++b) pending |= ((uint32_t)(v[b] >> 32) != tin) ? (1u << b) : 0u;
+      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
       if (!poll_step(spins, L, ctl)) break;
 #pragma unroll
-      for (int b = 0; b < B; ++b)
-        if (pending & (1u << b)) v[b] = ll_load(in + base + b * NL);
+      for (int b = 0; b < kFB; ++b)
+        if (pending & (1u << b)) v[b] = ll_load(in + at[b]);
     }
 #pragma unroll
-    for (int b = 0; b < B; ++b) {
-      const int idx = base + b * NL;
-      if (idx < nin) {
+    for (int b = 0; b < kFB; ++b) {
+      const int idx = at[b];
+      if (idx >= 0) {
         const uint32_t data = (uint32_t)v[b];
         const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
         if (w < 8)
@@ -233,34 +222,13 @@ __device__ __forceinline__ void fetch_input(const OpDev& op, Lds& L, int lid, Ct
       }
     }
   }
-  if (nold == 0) return;
-  uint32_t spins = 0;
-  for (;;) {
-    uint32_t pending = 0;
-#pragma unroll
-    for (int b = 0; b < kOld; ++b) pending |= ((uint32_t)(vo[b] >> 32) != told) ? (1u << b) : 0u;
-    if (pending == 0) break;
-    if (!poll_step(spins, L, ctl)) break;
-#pragma unroll
-    for (int b = 0; b < kOld; ++b) {
-      if (pending & (1u << b)) {
-        const int k = lid + b * NL;
-        vo[b] = ll_load(old + (first + (k >> 5) * G) * 32 + (k & 31));
-      }
-    }
-  }
-#pragma unroll
-  for (int b = 0; b < kOld; ++b) {
-    const int k = lid + b * NL;
-    if (k < nold) L.oldv[ob][k] = __uint_as_float((uint32_t)vo[b]);  // rows past N: unused
-  }
 }
 
-// The input fetch split in two for the I/O waves (kIW waves, one round, no
-// old values): the loads of an op whose input is at most kIL * kEIn words are
-// issued while the previous op computes and finished (poll what was stale,
-// write LDS) after that op's partial sums are in; its compute waves then
-// skip the fetch.
+// The input fetch of an "early" op by the I/O waves (kIW waves, one round):
+// its producers all come before the previous op, so the loads are issued
+// while the previous op computes and finished (poll what was stale, write
+// LDS) once that op's partial sums are in; each I/O wave then records the op
+// in L.early_seq, which the compute waves wait for instead of fetching.
 constexpr int kIL = 64 * kIW;
 constexpr int kEIn = 13;  // input words per lane: K <= 5324
 struct EarlyFetch {
@@ -339,11 +307,14 @@ __device__ __forceinline__ OpR op_r(const Lds& L, int i) {
   return r;
 }
 
-// Work of an op inside a workgroup: items (K-slice s, row quad q), s < S
-// (S = 1024-column slices), q < Q (the workgroup's quads: 4 rows, or for
-// swiglu 2 gate + 2 up rows), in slice-major order t = s*Q + q. One item is
-// one 16-byte code chunk (64 columns) per lane: lane l reads chunk
-// s*16 + (l & 15) of row quad row + (l >> 4).
+// Work of an op inside a workgroup: items (unit u, K-slice s, row quad q),
+// u < the workgroup's units of the op, s < S (1024-column slices), q < Qu
+// (quads of a unit: 4 rows each, or for swiglu 2 gate + 2 up rows), in the
+// order t = (u*S + s)*Qu + q: a unit's items are consecutive, so the I/O
+// waves can publish each unit as soon as it is done, and the items of a
+// compute wave touch few slices of the input. One item is one 16-byte code
+// chunk (64 columns) per lane: lane l reads chunk s*16 + (l & 15) of row
+// quad row + (l >> 4).
 struct Slot {
   u32x4 c;
   _Float16 s;  // fp16 scale of the chunk's 128-column block
@@ -357,9 +328,9 @@ struct Slot {
 struct OpWork {
   int i;  // op index (>= nops: past the program's end; every entry is a dummy)
   OpR op;
-  int S, Q, first;  // slices, quads, first unit of this workgroup
-  int t0, n, P;     // the wave's first item, real items, entries (a multiple of kRing)
-  int s0, q0;       // (s, q) of item t0
+  int S, Qu, Q, first;  // slices, quads per unit, quads of the workgroup, first unit
+  int t0, n, P;         // the wave's first item, real items, entries (a multiple of kRing)
+  int u0, s0, q0;       // (u, s, q) of item t0
 };
 // Every field is assigned on every path (a partly assigned struct would be
 // kept in scratch memory, whose accesses count in vmcnt).
@@ -371,22 +342,50 @@ __device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int 
   w.first = first_unit(w.op.rot, wg, G);
   const int nunits = past ? 0 : units_of(w.op.units, w.first, G);
   w.S = (w.op.cpr + 15) >> 4;
+  w.Qu = 1 << w.op.qpu_log2;
   w.Q = nunits << w.op.qpu_log2;
-  const int T = w.S * w.Q;
-  // Batches go to consecutive waves (wave w sits on SIMD w % 4), the first
-  // B % kCW waves taking one more, so the busy waves of a small op are spread
-  // over all four SIMDs.
+  const int U = w.S << w.op.qpu_log2;  // items per unit
+  const int T = nunits * U;
+  // Batches are balanced over the four SIMDs, not over the waves: wave w
+  // sits on SIMD w % 4, SIMDs 0 and 1 hold three compute waves and SIMDs 2
+  // and 3 two (beside the I/O waves), and a SIMD's waves mostly run one after
+  // another (the oldest issues first), so an op ends when its busiest SIMD
+  // does. SIMD k takes B/4 batches (the first B % 4 SIMDs one more), split
+  // over its waves the same way; runs follow in SIMD-major wave order.
   const int B = (T + kRing - 1) / kRing;
-  const int base = B / kCW, rem = B % kCW;
-  const int b0 = wave * base + (wave < rem ? wave : rem);
-  const int b1 = b0 + base + (wave < rem ? 1 : 0);
+  const int simd = wave & 3, slot = wave >> 2;         // slot: the wave's rank on its SIMD
+  const int nws = simd < kCW - 8 ? 3 : 2;              // compute waves on this SIMD
+  const int bs = B / 4 + (simd < B % 4 ? 1 : 0);       // batches of this SIMD
+  const int sb0 = simd * (B / 4) + (simd < B % 4 ? simd : B % 4);  // its first batch
+  const int b0 = sb0 + slot * (bs / nws) + (slot < bs % nws ? slot : bs % nws);
+  const int b1 = b0 + bs / nws + (slot < bs % nws ? 1 : 0);
   w.t0 = b0 * kRing;
   const int t1 = b1 * kRing < T ? b1 * kRing : T;
   w.n = t1 > w.t0 ? t1 - w.t0 : 0;
   w.P = (b1 > b0 ? b1 - b0 : 1) * kRing;
-  w.s0 = w.Q ? w.t0 / w.Q : 0;
-  w.q0 = w.t0 - w.s0 * w.Q;
+  const int ua = U ? w.t0 / U : 0, ra = w.t0 - ua * U;
+  w.u0 = ua;
+  w.s0 = ra >> w.op.qpu_log2;
+  w.q0 = ra & (w.Qu - 1);
   return w;
+}
+
+// The input slices the wave's real items read, as input LL word ranges
+// [a0, a1) and [b0, b1) (one of them, or both, may be empty): the items run
+// from (u0, s0) to the last one's (ub, sb).
+__device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, int& b0, int& b1) {
+  constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
+  const int U = w.S << w.op.qpu_log2;
+  const int tl = w.t0 + w.n - 1;
+  const int ub = tl / U, sb = (tl - ub * U) >> w.op.qpu_log2;
+  a0 = a1 = b0 = b1 = 0;
+  if (ub == w.u0) {
+    a0 = w.s0 * kWS, a1 = (sb + 1) * kWS;
+  } else if (ub == w.u0 + 1 && sb + 1 < w.s0) {
+    a0 = w.s0 * kWS, a1 = w.S * kWS, b1 = (sb + 1) * kWS;
+  } else {
+    a1 = w.S * kWS;
+  }
 }
 
 // Per-op, per-lane part of the load addresses: the lane's matrix (swiglu: odd
@@ -408,26 +407,28 @@ __device__ __forceinline__ LaneAddr lane_addr(const OpR& op, int l16, int grp) {
   return a;
 }
 
-// (s, q) cursor advanced without divisions.
+// (u, s, q) cursor advanced without divisions.
 struct Cur {
-  int s, q;
+  int u, s, q;
 };
-__device__ __forceinline__ void cur_next(int Q, Cur& c) {
-  if (++c.q == Q) {
+__device__ __forceinline__ void cur_next(int Qu, int S, Cur& c) {
+  if (++c.q == Qu) {
     c.q = 0;
-    ++c.s;
+    if (++c.s == S) {
+      c.s = 0;
+      ++c.u;
+    }
   }
 }
 
-// Load item (s, q) into a ring slot, or (real == false) the lane's chunk of
+// Load item (u, s, q) into a ring slot, or (real == false) the lane's chunk of
 // the op's first quad and slice, so every refill is an unconditional load
 // into the slot's own registers. The item's offset is uniform (SGPRs); quads
 // past N (N % 4 == 0, swiglu N % 2 == 0: a quad is all in or all out) read
 // quad 0.
 __device__ __forceinline__ void issue_item(const OpR& op, const LaneAddr& la, int first, const Cur& c, bool real,
                                            int G, Slot& sl) {
-  const int ui = c.q >> op.qpu_log2, qq = c.q & ((1 << op.qpu_log2) - 1);
-  int row0 = (first + ui * G) * 32 + (op.mode == BTF_GEMV_SWIGLU ? 2 * qq : 4 * qq);
+  int row0 = (first + c.u * G) * 32 + (op.mode == BTF_GEMV_SWIGLU ? 2 * c.q : 4 * c.q);
   row0 = real && row0 < op.N ? row0 : 0;
   const int s = real ? c.s : 0;
   // 32-bit uniform offsets (a matrix is below 4 GB, checked on the host)
@@ -499,27 +500,36 @@ __device__ __forceinline__ Consumed consume(const Slot& sl, const uint32_t (&aq)
   return r;
 }
 // Finish an entry: scale, 16-lane DPP reduction, store of the slice's
-// partial sum of the row into LDS part[s][local row].
-__device__ __forceinline__ void finish(const Consumed& c, const float (&ad)[2], bool store, int part_idx, int l16,
-                                       Lds& L) {
+// partial sum of the row into LDS part[s][local row], then the wave's count
+// of done items of the unit (a plain store of a uniform value: LDS
+// operations of a wave complete in order, so the I/O waves see the partial
+// sums once they see the count).
+__device__ __forceinline__ void finish(const Consumed& c, const float (&ad)[2], bool store, int part_idx,
+                                       uint32_t* count, uint32_t done, int lane, Lds& L) {
   float p = ad[0] * (float)c.y0;
   p = fmaf(ad[1], (float)c.y1, p);
   float acc = c.f * p;
   acc = row16_sum(acc);
-  if (store && l16 == 0) L.part[part_idx] = acc;
+  if (store) {
+    if ((lane & 15) == 0) L.part[part_idx] = acc;
+    asm volatile("" ::: "memory");
+    *count = done;
+  }
 }
 
-// The compute waves' whole program. Per op: barrier A (input in LDS), the
-// op's batches of kRing entries, barrier B (partial sums in LDS). Entry e of
-// the op lives in ring slot e % kRing; consuming it refills the slot with
-// entry e + kRing of the op, and in the op's last batch (a separate copy of
-// the loop body) with entry e + kRing - P of the NEXT op: the ring stays full
-// across op boundaries (the next op's first loads are in flight while this op
-// finishes and while the wave waits at B and A), with no dummy loads to
-// drain. Each copy of the body is straight-line code with one unconditional
-// load pair per entry, so the compiler keeps each slot in fixed registers
-// with exact wait counts (vmcnt = loads in flight - 2). The activation stays
-// in registers and is reloaded from LDS when the slice changes.
+// The compute waves' whole program. Per op: wait for the input slices the
+// wave's items read (fetch them, or for an early op wait until the I/O waves
+// have), the op's batches of kRing entries, barrier B (every wave done with
+// the op). Entry e of the op lives in ring slot e % kRing; consuming it
+// refills the slot with entry e + kRing of the op, and in the op's last
+// batch (a separate copy of the loop body) with entry e + kRing - P of the
+// NEXT op: the ring stays full across op boundaries (the next op's first
+// loads are in flight while this op finishes and while the wave waits for
+// its input), with no dummy loads to drain. Each copy of the body is
+// straight-line code with one unconditional load pair per entry, so the
+// compiler keeps each slot in fixed registers with exact wait counts. The
+// activation stays in registers and is reloaded from LDS when the slice
+// changes.
 __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
                                               uint32_t base_tag) {
   const int l16 = lane & 15, grp = lane >> 4;
@@ -529,25 +539,42 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
   LaneAddr la_cur = lane_addr(cur.op, l16, grp);
   LaneAddr la_nxt = lane_addr(nxt.op, l16, grp);
   {
-    Cur c{cur.s0, cur.q0};
+    Cur c{cur.u0, cur.s0, cur.q0};
 #pragma unroll
     for (int r = 0; r < kRing; ++r) {
       issue_item(cur.op, la_cur, cur.first, c, r < cur.n, G, ring[r]);
-      cur_next(cur.Q, c);
+      cur_next(cur.Qu, cur.S, c);
     }
   }
   for (;;) {
     const int ob = cur.i & 1;  // LDS buffers of this op
-    // (an early op's input was fetched by the I/O waves before this barrier)
-    if (!sgpr(L.opd[cur.i].early))
-      fetch_input<64 * kCW, (kMaxK / 32 * kWordsPerBlock + 64 * kCW - 1) / (64 * kCW)>(L.opd[cur.i], L, wave * 64 + lane,
-                                                                                       ctl, base_tag, wg, G, ob);
-    lds_barrier();  // A: the op's input is in LDS
-    const int R = cur.Q * 4;  // rows (virtual: swiglu gate/up interleaved) of this workgroup
-    Cur cc{cur.s0, cur.q0};   // entry being consumed
-    Cur lc = cc;              // entry being loaded (kRing ahead)
+    if (cur.n > 0) {
+      if (sgpr(L.opd[cur.i].early)) {
+        // fetched by the I/O waves after the previous op's barrier B
+        uint32_t spins = 0;
+        for (;;) {
+          bool ready = true;
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) cur_next(cur.Q, lc);
+          for (int k = 0; k < kIW; ++k)
+            ready &= __hip_atomic_load(&L.early_seq[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+                     (uint32_t)cur.i + 1;
+          if (ready || !poll_step(spins, L, ctl)) break;
+        }
+        asm volatile("" ::: "memory");
+      } else {
+        int a0, a1, b0, b1;
+        input_words(cur, a0, a1, b0, b1);
+        fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0, b1);
+        // the words other lanes of this wave wrote are read below
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      }
+    }
+    const int R = cur.Q * 4;  // rows (virtual: swiglu gate/up interleaved) of this workgroup
+    const int U = cur.S << cur.op.qpu_log2;  // items per unit
+    Cur cc{cur.u0, cur.s0, cur.q0};  // entry being consumed
+    Cur lc = cc;                     // entry being loaded (kRing ahead)
+#pragma unroll
+    for (int r = 0; r < kRing; ++r) cur_next(cur.Qu, cur.S, lc);
     uint32_t aq[16];
     float ad[2];
     int an[2];
@@ -561,22 +588,23 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         __builtin_amdgcn_sched_barrier(0);
         issue_item(cur.op, la_cur, cur.first, lc, e + kRing < cur.n, G, ring[r]);
         __builtin_amdgcn_sched_barrier(0);
-        cur_next(cur.Q, lc);
-        finish(c, ad, e < cur.n, cc.s * R + cc.q * 4 + grp, l16, L);
+        cur_next(cur.Qu, cur.S, lc);
+        finish(c, ad, e < cur.n, cc.s * R + ((cc.u << cur.op.qpu_log2) + cc.q) * 4 + grp, &L.ucnt[wave][cc.u],
+               (uint32_t)(cur.t0 + e + 1 - max(cur.t0, cc.u * U)), lane, L);
         const int s_prev = cc.s;
-        cur_next(cur.Q, cc);
+        cur_next(cur.Qu, cur.S, cc);
         if (cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
     if (cur.n == 0) {  // no real entry: only the refills with the next op's first entries
-      Cur ln{nxt.s0, nxt.q0};
+      Cur ln{nxt.u0, nxt.s0, nxt.q0};
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
         issue_item(nxt.op, la_nxt, nxt.first, ln, r < nxt.n, G, ring[r]);
-        cur_next(nxt.Q, ln);
+        cur_next(nxt.Qu, nxt.S, ln);
       }
     } else {  // last batch: the refills load the next op's first entries
-      Cur ln{nxt.s0, nxt.q0};
+      Cur ln{nxt.u0, nxt.s0, nxt.q0};
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
         const int e = cur.P - kRing + r;
@@ -584,14 +612,15 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         __builtin_amdgcn_sched_barrier(0);
         issue_item(nxt.op, la_nxt, nxt.first, ln, r < nxt.n, G, ring[r]);
         __builtin_amdgcn_sched_barrier(0);
-        cur_next(nxt.Q, ln);
-        finish(c, ad, e < cur.n, cc.s * R + cc.q * 4 + grp, l16, L);
+        cur_next(nxt.Qu, nxt.S, ln);
+        finish(c, ad, e < cur.n, cc.s * R + ((cc.u << cur.op.qpu_log2) + cc.q) * 4 + grp, &L.ucnt[wave][cc.u],
+               (uint32_t)(cur.t0 + e + 1 - max(cur.t0, cc.u * U)), lane, L);
         const int s_prev = cc.s;
-        cur_next(cur.Q, cc);
+        cur_next(cur.Qu, cur.S, cc);
         if (r + 1 < kRing && cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
       }
     }
-    lds_barrier();  // B: the op's partial sums are in LDS
+    lds_barrier();  // B: every wave is done with the op
     if (nxt.i >= nops) break;
     cur = nxt;
     la_cur = la_nxt;
@@ -655,16 +684,49 @@ __device__ __forceinline__ void wait_readers(int war_op, const uint32_t* rd_cnt,
   }
 }
 
-__device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int G, int iol, uint32_t base_tag, int ob) {
+// Publish the op's units as the compute waves complete them: half-wave h
+// takes local units h, h + 4, ...; for each, it waits until the unit's
+// items are all counted (the compute waves' counts add up), reduces
+// part[slice][row] over the slices in order,
+// applies the mode (old value: the LDS carry, or the LL word of the previous
+// version, loaded one unit ahead) and publishes. Returns each counter to 0
+// for the next op.
+__device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int G, int iol, uint32_t base_tag,
+                                           Ctl* ctl) {
   const int half = iol >> 5, j = iol & 31, nhalves = kIW * 2;
   const int first = first_unit(sgpr(op.rot), wg, G);
   const int nunits = units_of(sgpr(op.units), first, G);
   const int mode = sgpr(op.mode), N = sgpr(op.N);
-  const int S = (sgpr(op.cpr) + 15) >> 4;  // 1024-column slices: partial sums per row
+  const int S = (sgpr(op.cpr) + 15) >> 4;                      // 1024-column slices: partial sums per row
+  const uint32_t items = (uint32_t)S << sgpr(op.qpu_log2);     // items per unit
   const int R = nunits * (mode == BTF_GEMV_SWIGLU ? 64 : 32);  // rows of part[slice][row]
   const uint32_t tag = base_tag + sgpr(op.my_tag);
   const bool carry_in = sgpr(op.carry_in), carry_out = sgpr(op.carry_out);
+  const bool old_ll = mode == BTF_GEMV_ADD && !carry_in;
+  const uint64_t* old = sgpr_ptr(op.old_f32);
+  const uint32_t told = base_tag + sgpr(op.old_tag);
+  auto old_word = [&](int ui) {
+    const int row = (first + ui * G) * 32 + j;
+    return (old_ll && ui < nunits && row < N) ? ll_load(old + row) : ((uint64_t)told << 32);
+  };
+  uint64_t ov = old_word(half);
   for (int ui = half; ui < nunits; ui += nhalves) {
+    {
+      // polled at normal priority and sparsely: the compute waves on the
+      // same SIMDs are producing these items
+      __builtin_amdgcn_s_setprio(0);
+      uint32_t spins = 0;
+      for (;;) {
+        uint32_t done = 0;
+#pragma unroll
+        for (int w = 0; w < kCW; ++w) done += __hip_atomic_load(&L.ucnt[w][ui], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if (done == items || !poll_step(spins, L, ctl)) break;
+        __builtin_amdgcn_s_sleep(3);
+      }
+      __builtin_amdgcn_s_setprio(3);
+    }
+    asm volatile("" ::: "memory");
+    if (j < kCW) __hip_atomic_store(&L.ucnt[j][ui], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int unit = first + ui * G;
     const int row = unit * 32 + j;
     const bool valid = row < N;
@@ -672,22 +734,39 @@ __device__ __forceinline__ void io_epilogue(const OpDev& op, Lds& L, int wg, int
     if (mode == BTF_GEMV_SWIGLU) {
       const int lr = ui * 64 + 2 * j;  // virtual rows: gate 2j, up 2j+1 of this unit
       float g = 0.f, u = 0.f;
-      for (int k = 0; k < S; ++k) {
-        g += L.part[k * R + lr];
-        u += L.part[k * R + lr + 1];
+      for (int s = 0; s < S; ++s) {
+        g += L.part[s * R + lr];
+        u += L.part[s * R + lr + 1];
       }
       v = g / (1.0f + expf(-g)) * u;
     } else {
       const int lr = ui * 32 + j;
       float sum = 0.f;
-      for (int k = 0; k < S; ++k) sum += L.part[k * R + lr];
-      v = mode == BTF_GEMV_ADD ? (carry_in ? L.carry[lr] : L.oldv[ob][lr]) + sum : sum;
+      for (int s = 0; s < S; ++s) sum += L.part[s * R + lr];
+      if (mode == BTF_GEMV_ADD) {
+        float o;
+        if (carry_in) {
+          o = L.carry[lr];
+        } else {
+          uint32_t spins = 0;
+          while ((uint32_t)(ov >> 32) != told && poll_step(spins, L, ctl)) ov = ll_load(old + row);
+          o = __uint_as_float((uint32_t)ov);
+          ov = old_word(ui + nhalves);  // the next unit's, in flight while it computes
+        }
+        v = o + sum;
+      } else {
+        v = sum;
+      }
       if (carry_out) L.carry[lr] = v;
     }
     publish_unit(op, unit, j, valid ? v : 0.f, valid, tag);
   }
 }
 
+// The I/O waves' program. Per op: issue the early loads of the next op's
+// input (if it is early), wait for the write-after-read guard, publish the
+// units as they complete, barrier B, count this workgroup's reads of the
+// op's input, finish the early fetch.
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
                                          uint32_t base_tag) {
   for (int i = 0; i < nops; ++i) {
@@ -696,20 +775,21 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       io_quantize(op, wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
-    lds_barrier();  // A: the op's input is in LDS
-    if (sgpr(op.count_reads) && iol == 0)
-      (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The next op's input, when its producers all come before op i (no
-    // workgroup then waits on op i): loads issued while op i computes,
-    // finished after B (its buffer is free then), before op i's epilogue.
     const int nx = sgpr(op.next);
     const bool early = nx < nops && sgpr(L.opd[nx].early);
     EarlyFetch ef;
     if (early) early_issue(L.opd[nx], iol, base_tag, ef);
     wait_readers(sgpr(op.war_op), rd_cnt, G, L, ctl);
-    lds_barrier();  // B: the compute waves' partial sums are in LDS
-    if (early) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl);
-    io_epilogue(op, L, wg, G, iol, base_tag, i & 1);
+    io_publish(op, L, wg, G, iol, base_tag, ctl);
+    lds_barrier();  // B: every compute wave is done with the op's input
+    if (sgpr(op.count_reads) && iol == 0)
+      (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (early) {
+      early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the input words are in LDS
+      if ((iol & 63) == 0)
+        __hip_atomic_store(&L.early_seq[iol >> 6], (uint32_t)nx + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
   }
 }
 
@@ -726,6 +806,8 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
     const int nvec = nops * (int)(sizeof(OpDev) / 16);
     for (int k = threadIdx.x; k < nvec; k += kThreads) dst[k] = src[k];
   }
+  for (int k = threadIdx.x; k < kCW * kMaxUnits; k += kThreads) (&L.ucnt[0][0])[k] = 0;
+  if (threadIdx.x < kIW) L.early_seq[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
     L.epoch = ctl_load(&ctl->epoch);
     const uint32_t sm = ctl_load(&ctl->spin_max);
@@ -905,13 +987,15 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
   auto f32_of = [&](int v, int k) { return versions[v][k].f32_slot >= 0 ? f32buf[versions[v][k].f32_slot][v] : nullptr; };
   // ---- the device program: prologue quantize ops, then the GEMVs in order
   std::vector<OpDev> ops;
-  // seen[w]: the last GEMV whose input workgroup w has surely fetched before
-  // any workgroup passes the current op's input barrier. A workgroup passes
-  // an op's input barrier after every word of its input was published, and
-  // each publisher w had fetched the inputs of every op up to that producer
-  // first; a workgroup passes the barriers of all earlier ops before this
-  // one, so what they implied holds too (a running maximum).
-  std::vector<int> seen(G, -1);
+  // known[v * G + w]: the last GEMV whose barrier B workgroup w has surely
+  // passed, as far as workgroup v can tell when it reaches a later op. A
+  // workgroup that owns units of an op reads all of its input (every unit
+  // spans all slices), published unit by unit by the writers of the input's
+  // producer X, each of which had passed B of the GEMV before X. Workgroup v
+  // has passed B of every earlier op before starting an op.
+  std::vector<int> known((size_t)G * G, -1);
+  int last_gemv = -1;                   // device index of the previous GEMV
+  std::vector<int> prev_gemv;           // per device op: the GEMV before it (-1: none)
   auto owns = [&](const OpDev& x, int w) { return (w - x.rot + G) % G < x.units; };
   std::vector<int> dev_of(ngemv, -1);        // device op index of each GEMV
   std::vector<int> prologue_of(nvec, -1);    // device op index of each prologue op
@@ -961,6 +1045,7 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     place(o, 1.0, -1);
     prologue_of[v] = (int)ops.size();
     ops.push_back(o);
+    prev_gemv.push_back(-1);
   }
   auto dev_writer = [&](int v, int k) {
     const int w = versions[v][k].writer;
@@ -1029,14 +1114,27 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
       for (int r : v0.f32_readers) last = std::max(last, r);
       if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
     }
+    if (war >= 0) {  // implied for every workgroup that writes this op's output?
+      bool implied = true;
+      for (int v = 0; v < G && implied; ++v) {
+        if (!owns(o, v)) continue;
+        for (int w = 0; w < G; ++w)
+          if (w != v && known[(size_t)v * G + w] < war) {
+            implied = false;
+            break;
+          }
+      }
+      if (implied) war = -1;
+    }
     {
       const int x = (int)o.in_tag - 1;  // input producer
-      int low = INT_MAX;
-      for (int w = 0; w < G; ++w) {
-        if (ops[x].kind == 1 && owns(ops[x], w)) seen[w] = std::max(seen[w], x);
-        low = std::min(low, seen[w]);
-      }
-      if (war >= 0 && low >= war) war = -1;  // implied by the barriers passed so far
+      const int px = x < (int)prev_gemv.size() ? prev_gemv[x] : -1;
+      if (ops[x].kind == 1 && px >= 0)
+        for (int v = 0; v < G; ++v) {
+          if (!owns(o, v)) continue;
+          for (int w = 0; w < G; ++w)
+            if (owns(ops[x], w)) known[(size_t)v * G + w] = std::max(known[(size_t)v * G + w], px);
+        }
     }
     o.war_op = war;
     if (war >= 0) ops[war].count_reads = 1;
@@ -1047,6 +1145,8 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     if (g.mode == BTF_GEMV_ADD && max_units * 32 > kMaxOld)
       return bail(BTF_ERR_ARGS, "step: add-mode output too tall for the old-value buffer");
     ops.push_back(o);
+    prev_gemv.push_back(last_gemv);
+    last_gemv = me;
   }
   if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 384 ops (quantize prologue + GEMVs)");
   // Early fetch and carry. An op's input is fetched by the I/O waves while
