@@ -498,6 +498,14 @@ def main():
             per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
                          "launches_per_step": 1 if kind == "output" else layers}
             log(f"  op-by-op {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    # FETCH_SIZE / WRITE_SIZE runs (profiles/hbm_traffic.json), when they
+    # cover this engine's dominant kernel; counters cannot be read live.
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            traffic_tab = json.load(f)
+    except (OSError, ValueError):
+        traffic_tab = {}
     if engine == "step":
         roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
@@ -507,8 +515,10 @@ def main():
         dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
         d = per[dom]
         if step.M <= 32:
+            tr = traffic_tab.get(f"{engine}/{dom}") if step.M == 1 and args.workload == "sweep" else None
             roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                    "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
+                    "traffic_source": tr["source"] if tr else None,
                     "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'}"
                               f"{', quantizes fused in' if fk else ''})",
                     "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
