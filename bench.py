@@ -498,6 +498,37 @@ def main():
             per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
                          "launches_per_step": 1 if kind == "output" else layers}
             log(f"  op-by-op {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
+    # The kernels either side of the GEMV chain (not part of the sweep's
+    # value): the embedding lookup of one token from a packed table of the
+    # output projection's shape (V x 5120, with the inverse transform at
+    # block 1024 + signs), the greedy pick over V logits (two launches) and
+    # the position counter; graphs of 64 launches each, per-launch average.
+    ends = None
+    if step.with_output and args.workload == "sweep":
+        N_, K_, _, co, so = S.mats[("output", layers)]
+        base = S.arena.data_ptr()
+        toks = torch.arange(64, dtype=torch.int32, device="cuda") * 3877 % V
+        signs = torch.where(torch.rand(E, device="cuda") < 0.5, -1.0, 1.0).to(torch.float32)
+        xe = torch.zeros((1, E), dtype=torch.float32, device="cuda")
+        inv = hip.Hx(block=1024, signs=signs)
+        part = torch.zeros(hip.argmax_part_bytes(V) // 4, dtype=torch.int32, device="cuda")
+        tok_out = torch.zeros(1, dtype=torch.int32, device="cuda")
+        pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+        tp = toks.data_ptr()
+        fns = {
+            "embed": lambda st: [hip.launch_embed(base + co, base + so, tp + 4 * i, 1, E, inv, xe, st) for i in range(64)],
+            "argmax": lambda st: [hip.launch_argmax(step.logits, V, part, tok_out, st) for _ in range(64)],
+            "pos_add": lambda st: [hip.launch_pos_add(pos, 1, st) for _ in range(64)],
+        }
+        ends = {}
+        for name, fn in fns.items():
+            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            ends[f"{name}_us"] = round(kms * 1e3 / 64, 3)
+        ends["embed_bytes"] = E // 4 + E // 64 + 4 * E
+        ends["argmax_bytes"] = 4 * V
+        log(f"decode-step ends: embed {ends['embed_us']} us, argmax {ends['argmax_us']} us "
+            f"({ends['argmax_bytes'] / (ends['argmax_us'] * 1e3):.1f} GB/s), pos_add {ends['pos_add_us']} us")
+
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE runs (profiles/hbm_traffic.json), when they
     # cover this engine's dominant kernel; counters cannot be read live.
@@ -563,6 +594,7 @@ def main():
         "verified": {"vs_graph_engine_bit_exact": verified} if verified else None,
         "engines_ms": {k: round(v, 4) for k, v in engine_ms.items()},
         "gemv_kinds": per,
+        "decode_step_ends": ends,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},
     }
     if not args.no_cpu:

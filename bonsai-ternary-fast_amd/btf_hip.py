@@ -74,6 +74,10 @@ _launch_repack = _decl("btf_hip_launch_repack", [_vp, _i64, _vp, _vp, _vp])
 _launch_prep = _decl("btf_hip_launch_prep",
                      [_vp, _i, _i, _i, _vp, C.c_float, C.POINTER(_Hx), _vp, _i, C.POINTER(_Q8Act), _vp])
 _launch_gemv = _decl("btf_hip_launch_gemv", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _i, _vp])
+_launch_embed = _decl("btf_hip_launch_embed", [_vp, _vp, _vp, _i, _i, C.POINTER(_Hx), _vp, _vp])
+_argmax_part_bytes = _decl("btf_hip_argmax_part_bytes", [_i], _i64)
+_launch_argmax = _decl("btf_hip_launch_argmax", [_vp, _i, _vp, _vp, _vp])
+_launch_pos_add = _decl("btf_hip_launch_pos_add", [_vp, _i, _vp])
 _launch_gemv_ex = _decl("btf_hip_launch_gemv_ex", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _vp, _i, _i,
                                                     C.POINTER(_Q8Act), _vp])
 _dump = _decl("btf_hip_gemv_i32_dump", [_vp, _i, _i, _i, C.POINTER(_Q8Act), _vp, _vp])
@@ -101,7 +105,8 @@ _step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
 #: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
 ABI_SYMBOLS = (
     "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
-    "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
+    "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_launch_embed", "btf_hip_argmax_part_bytes",
+    "btf_hip_launch_argmax", "btf_hip_launch_pos_add", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
     "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
     "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
     "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
@@ -206,6 +211,36 @@ def launch_gemv(segs, K: int, M: int, a: Q8Act, mode: GemvMode = GemvMode.kStore
     arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs])
     q = a._c()
     _check(_launch_gemv(arr, len(segs), K, M, C.byref(q), int(mode), _stream(stream)))
+
+
+def launch_embed(codes, scales, d_tok, M: int, E: int, inv: "Hx" = None, x=None, stream=None) -> None:
+    """src/cuda/kernels.cuh:82-85."""
+    h = (inv or Hx())._c()
+    _check(_launch_embed(_addr(codes), _addr(scales), _addr(d_tok), M, E, C.byref(h), _addr(x), _stream(stream)))
+
+
+def launch_embed_raw(codes, scales, d_tok, M, E, inv, x, stream=None) -> int:
+    h = (inv or Hx())._c()
+    return _launch_embed(_addr(codes), _addr(scales), _addr(d_tok), M, E, C.byref(h), _addr(x), _stream(stream))
+
+
+def argmax_part_bytes(V: int) -> int:
+    """src/cuda/kernels.cuh:89."""
+    return int(_argmax_part_bytes(V))
+
+
+def launch_argmax(logits, V: int, part, d_tok_out, stream=None) -> None:
+    """src/cuda/kernels.cuh:87-90."""
+    _check(_launch_argmax(_addr(logits), V, _addr(part), _addr(d_tok_out), _stream(stream)))
+
+
+def launch_argmax_raw(logits, V, part, d_tok_out, stream=None) -> int:
+    return _launch_argmax(_addr(logits), V, _addr(part), _addr(d_tok_out), _stream(stream))
+
+
+def launch_pos_add(d_pos, M: int, stream=None) -> None:
+    """src/cuda/kernels.cuh:92."""
+    _check(_launch_pos_add(_addr(d_pos), M, _stream(stream)))
 
 
 def launch_gemv_ex(segs, K: int, M: int, a: Q8Act = None, x=None, ldx: int = 0,

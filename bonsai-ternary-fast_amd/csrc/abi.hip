@@ -184,6 +184,41 @@ int btf_hip_launch_gemv(const btf_gemv_seg* segs, int nseg, int K, int M, const 
   return run_gemv(segs, nseg, K, M, a, mode, nullptr, static_cast<hipStream_t>(stream));
 }
 
+int btf_hip_launch_embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E,
+                         const btf_hx* inv, float* x, btf_stream_t stream) {
+  if (M <= 0) return BTF_OK;
+  if (!codes || !scales || !d_tok || !x) return fail(BTF_ERR_ARGS, "embed: null pointer");
+  if (E <= 0 || E % 128) return fail(BTF_ERR_ARGS, "embed: width must be a multiple of 128");
+  if (!aligned(codes, 4) || !aligned(scales, 2)) return fail(BTF_ERR_ARGS, "embed: codes must be 4-byte aligned");
+  const int block = inv ? inv->block : 0;
+  if (block < 0 || (block > 0 && (block & (block - 1))))
+    return fail(BTF_ERR_ARGS, "embed: hadamard block must be 0 or a power of two");
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  return embed(codes, scales, d_tok, M, E, block, inv ? inv->signs : nullptr, x, static_cast<hipStream_t>(stream));
+}
+
+int64_t btf_hip_argmax_part_bytes(int V) {
+  (void)V;
+  return argmax_part_bytes();
+}
+
+int btf_hip_launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t stream) {
+  if (!logits || !part || !d_tok_out) return fail(BTF_ERR_ARGS, "argmax: null pointer");
+  if (V <= 0) return fail(BTF_ERR_ARGS, "argmax: empty vocabulary");
+  if (!aligned(part, 8)) return fail(BTF_ERR_ARGS, "argmax: part must be 8-byte aligned");
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  return argmax(logits, V, part, d_tok_out, static_cast<hipStream_t>(stream));
+}
+
+int btf_hip_launch_pos_add(int* d_pos, int M, btf_stream_t stream) {
+  if (!d_pos) return fail(BTF_ERR_ARGS, "pos_add: null pointer");
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  return pos_add(d_pos, M, static_cast<hipStream_t>(stream));
+}
+
 int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, const float* x,
                            int ldx, int mode, const btf_q8act* out, btf_stream_t stream) {
   if (M <= 0) return BTF_OK;

@@ -256,9 +256,10 @@ __device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t 
     for (int b = 0; b < kEIn; ++b) pending |= ((uint32_t)(f.v[b] >> 32) != tin) ? (1u << b) : 0u;
     if (pending == 0) break;
     if (!poll_step(spins, L, ctl)) break;
-#pragma unroll
-    for (int b = 0; b < kEIn; ++b)
-      if (pending & (1u << b)) f.v[b] = ll_load(in + lid + b * kIL);
+    for (int b = 0; b < kEIn; ++b) {
+      const int idx = lid + b * kIL;
+      if ((pending & (1u << b)) && idx < nin) f.v[b] = ll_load(in + idx);
+    }
   }
 #pragma unroll
   for (int b = 0; b < kEIn; ++b) {

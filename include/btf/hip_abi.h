@@ -98,6 +98,29 @@ int btf_hip_launch_prep(const float* x, int ldx, int M, int n, const float* norm
 int btf_hip_launch_gemv(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, int mode,
                         btf_stream_t stream);
 
+/* Replaces btf::cuda::launch_embed (kernels.cuh:82-85): rows d_tok[0..M) of
+ * the packed embedding table (codes [V][E/4], scales [V][E/128] in the T2
+ * layout; device or mapped host memory) -> x [M][E] fp32, then the inverse
+ * transform: inv NULL or inv->block == 0 for none, else a blockwise
+ * normalised FWHT (x 1/sqrt(block)) and, if inv->signs is set, the signs.
+ * E % 128 == 0. Token ids must lie in [0, V): as in the reference, V is not a
+ * parameter and the ids are device data, so the launch cannot check them. */
+int btf_hip_launch_embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E,
+                         const btf_hx* inv, float* x, btf_stream_t stream);
+
+/* Replaces btf::cuda::argmax_part_bytes (kernels.cuh:89): scratch bytes
+ * launch_argmax needs in `part`. */
+int64_t btf_hip_argmax_part_bytes(int V);
+
+/* Replaces btf::cuda::launch_argmax (kernels.cuh:87-90): greedy pick over
+ * logits[0..V) (the smallest index on ties; NaN never wins) -> *d_tok_out.
+ * part: btf_hip_argmax_part_bytes(V) bytes of device scratch, 8-byte
+ * aligned. */
+int btf_hip_launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t stream);
+
+/* Replaces btf::cuda::launch_pos_add (kernels.cuh:92): *d_pos += M. */
+int btf_hip_launch_pos_add(int* d_pos, int M, btf_stream_t stream);
+
 /* Message of the last failure on this thread ("" if none). */
 const char* btf_hip_last_error(void);
 

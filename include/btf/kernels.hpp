@@ -80,6 +80,24 @@ inline void launch_gemv(const GemvSeg* segs, int nseg, int K, int M, const Q8Act
   detail::check(btf_hip_launch_gemv(s, nseg, K, M, &q, mode, st), "launch_gemv");
 }
 
+// kernels.cuh:82-85
+inline void launch_embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E, const Hx& inv,
+                         float* x, btf_stream_t st) {
+  const btf_hx h{inv.block, inv.perm_hd, inv.perm_nk, inv.perm_rep, inv.signs};
+  detail::check(btf_hip_launch_embed(codes, scales, d_tok, M, E, &h, x, st), "launch_embed");
+}
+
+// kernels.cuh:89-90
+inline size_t argmax_part_bytes(int V) { return (size_t)btf_hip_argmax_part_bytes(V); }
+inline void launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t st) {
+  detail::check(btf_hip_launch_argmax(logits, V, part, d_tok_out, st), "launch_argmax");
+}
+
+// kernels.cuh:92
+inline void launch_pos_add(int* d_pos, int M, btf_stream_t st) {
+  detail::check(btf_hip_launch_pos_add(d_pos, M, st), "launch_pos_add");
+}
+
 // launch_gemv with the chain's quantizes fused in (no counterpart in
 // kernels.cuh: the decoder's launch_prep + launch_gemv pairs without norm or
 // transform, src/cuda/gpu_decoder.cu:411-418): input from Q8 rows `a` or fp32

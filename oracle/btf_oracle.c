@@ -505,6 +505,40 @@ void btf_or_swiglu(float* g, const float* u, int64_t n) {
 }
 
 /* ======================================================================
+ * either side of the GEMV chain
+ * ====================================================================== */
+
+/* src/emu_decoder.cpp:171-180 with ref/bonsai-decoder/src/cpu_ops.cpp:113-118.
+ * The emulator applies hadamard_inverse only when the transform is active
+ * (block > 0): then each block gets the normalised FWHT and, if present, the
+ * whole row is multiplied by the signs. */
+int btf_or_embed(const uint8_t* codes, const uint16_t* scales, const int32_t* toks, int M, int E, int V, int block,
+                 const float* signs, float* x) {
+  for (int m = 0; m < M; ++m) {
+    const int tok = toks[m];
+    if (tok < 0 || tok >= V) return -1;
+    const uint8_t* cr = codes + (int64_t)tok * (E / 4);
+    const uint16_t* sr = scales + (int64_t)tok * (E / 128);
+    float* xr = x + (int64_t)m * E;
+    for (int i = 0; i < E; ++i) xr[i] = (float)(btf_or_packed_code(cr, i) - 1) * btf_or_fp16_to_f32(sr[i / 128]);
+    if (block > 0) {
+      for (int b = 0; b < E; b += block) btf_or_fwht(xr + b, block);
+      if (signs)
+        for (int i = 0; i < E; ++i) xr[i] *= signs[i];
+    }
+  }
+  return 0;
+}
+
+/* ref/bonsai-decoder/src/sampler.cpp:20-25: keep the first maximum (strict >). */
+int btf_or_argmax(const float* logits, int n) {
+  int best = 0;
+  for (int i = 1; i < n; ++i)
+    if (logits[i] > logits[best]) best = i;
+  return best;
+}
+
+/* ======================================================================
  * seeded synthetic weights
  * ====================================================================== */
 

@@ -103,6 +103,18 @@ void btf_or_gemv(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_
  * g = silu(g) * u (src/emu_decoder.cpp:195-197). */
 void btf_or_swiglu(float* g, const float* u, int64_t n);
 
+/* ---- either side of the GEMV chain -------------------------------------- */
+/* Embedding lookup: src/emu_decoder.cpp:171-180 (row decode of the packed
+ * table: (code - 1) * fp16 scale) then bd::hadamard_inverse
+ * (ref/bonsai-decoder/src/cpu_ops.cpp:113-118: normalised FWHT per block, then
+ * the signs). block == 0: no transform. toks [M] in [0, V), else -1 (the
+ * emulator throws); x [M][E]. */
+int btf_or_embed(const uint8_t* codes, const uint16_t* scales, const int32_t* toks, int M, int E, int V, int block,
+                 const float* signs, float* x);
+/* Greedy pick: ref/bonsai-decoder/src/sampler.cpp:20-25 (and the emulator's
+ * own loop, src/emu_decoder.cpp:205-207): the first index of the maximum. */
+int btf_or_argmax(const float* logits, int n);
+
 /* ---- seeded synthetic weights (the benchmark's generator) ------------- */
 /* nblocks PTQ1_0 blocks of matrix `mat`: trits i.i.d. with
  * P(-1,0,+1) = (0.3,0.4,0.3), fp16 scale = RNE(U[0.01,0.05]). Block b's

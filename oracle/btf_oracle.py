@@ -66,6 +66,8 @@ class Oracle:
         _decl(L, "btf_or_gemv_i32", None, [_p, _i64, _i64, _p, _p, _i32, _p])
         _decl(L, "btf_or_gemv", None, [_p, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i32, _i32])
         _decl(L, "btf_or_swiglu", None, [_p, _p, _i64])
+        _decl(L, "btf_or_embed", _i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _p, _p])
+        _decl(L, "btf_or_argmax", _i32, [_p, _i32])
         _decl(L, "btf_or_gen_ptq1_0", None, [C.c_uint64, C.c_uint64, _i64, _i64, _p])
         _decl(L, "btf_or_hw_threads", _i32, [])
 
@@ -194,6 +196,22 @@ class Oracle:
         self.lib.btf_or_swiglu(_ptr(g), _ptr(u), g.size)
         return g
 
+    # ---- either side of the chain (src/emu_decoder.cpp:171-180, 205-207;
+    # ref/bonsai-decoder/src/sampler.cpp:20-25)
+    def embed(self, codes, scales, toks, E, V, block=0, signs=None):
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales).view(np.uint16)
+        toks = np.ascontiguousarray(toks, np.int32)
+        sg = None if signs is None else np.ascontiguousarray(signs, np.float32)
+        x = np.zeros((toks.size, E), np.float32)
+        if self.lib.btf_or_embed(_ptr(codes), _ptr(scales), _ptr(toks), toks.size, E, V, block, _ptr(sg), _ptr(x)):
+            raise ValueError("embed: token id out of range")
+        return x
+
+    def argmax(self, logits) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return self.lib.btf_or_argmax(_ptr(logits), logits.size)
+
     def hw_threads(self) -> int:
         return self.lib.btf_or_hw_threads()
 
@@ -226,6 +244,8 @@ class Ref:
         _decl(L, "ref_emu_gemv_timed", C.c_double, [_p, _p, _i64, _i64, _p, _p, _p, _i32, _p, _i64, _i32, _i32])
         _decl(L, "ref_emu_prep", _i32,
               [_p, _i32, _i32, _p, C.c_float, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p])
+        _decl(L, "ref_emu_embed", _i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _p, _p])
+        _decl(L, "ref_argmax", _i32, [_p, _i32])
 
     def quant_ptq1_0(self, w):
         w = np.ascontiguousarray(w, np.float32)
@@ -314,6 +334,20 @@ class Ref:
         if rc != 0:
             raise ValueError("ref_emu_prep failed")
         return q, d, s, xn
+
+    def emu_embed(self, codes, scales, toks, E, V, block=0, signs=None):
+        codes = np.ascontiguousarray(codes, np.uint8)
+        scales = np.ascontiguousarray(scales).view(np.uint16)
+        toks = np.ascontiguousarray(toks, np.int32)
+        sg = None if signs is None else np.ascontiguousarray(signs, np.float32)
+        x = np.zeros((toks.size, E), np.float32)
+        if self.lib.ref_emu_embed(_ptr(codes), _ptr(scales), _ptr(toks), toks.size, E, V, block, _ptr(sg), _ptr(x)):
+            raise ValueError("embed: token id out of range")
+        return x
+
+    def argmax(self, logits) -> int:
+        logits = np.ascontiguousarray(logits, np.float32)
+        return self.lib.ref_argmax(_ptr(logits), logits.size)
 
 
 def have_ref() -> bool:

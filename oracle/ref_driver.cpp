@@ -30,6 +30,7 @@
 #include "bd/cpu_ops.hpp"
 #include "bd/gguf.hpp"
 #include "bd/model.hpp"
+#include "bd/sampler.hpp"
 #include "bd/synth.hpp"
 #include "bd/types.hpp"
 #include "btf/fast.hpp"
@@ -160,6 +161,39 @@ double ref_emu_gemv_timed(const uint8_t* codes, const uint16_t* scales, int64_t 
     return -1.0;
   }
 }
+
+// The emulator's embedding lookup (src/emu_decoder.cpp:171-180): the same
+// calls on rows of a packed table -- btf::packed_code, bd::fp16_to_f32 and
+// bd::hadamard_inverse with the emulator's transform (active when block > 0).
+int ref_emu_embed(const uint8_t* codes, const uint16_t* scales, const int32_t* toks, int M, int E, int V, int block,
+                  const float* signs, float* x) {
+  try {
+    std::vector<float> sg;
+    bd::HadamardXform hx;
+    hx.active = block > 0;
+    hx.block = block;
+    if (signs) {
+      sg.assign(signs, signs + E);
+      hx.signs = &sg;
+    }
+    for (int m = 0; m < M; ++m) {
+      const int tok = toks[m];
+      if (tok < 0 || tok >= V) throw std::runtime_error("token id out of range");
+      float* xr = x + (size_t)m * E;
+      const uint8_t* cr = codes + (size_t)tok * (E / 4);
+      const uint16_t* sr = scales + (size_t)tok * (E / 128);
+      for (int i = 0; i < E; ++i) xr[i] = (float)(btf::packed_code(cr, i) - 1) * bd::fp16_to_f32(sr[i / 128]);
+      bd::hadamard_inverse(hx, xr, E);
+    }
+    return 0;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "ref_emu_embed: %s\n", e.what());
+    return -1;
+  }
+}
+
+// The greedy sampler (ref/bonsai-decoder/src/sampler.cpp:20-25).
+int ref_argmax(const float* logits, int n) { return bd::Sampler::argmax(logits, n); }
 
 // The emulator's fused prep (src/emu_decoder.cpp:122-140) on dense rows
 // x [M][n]; block == 0 means no input transform.

@@ -18,6 +18,9 @@ produced by a reference function:
   mv_y                  bd::matvec_raw(ggml_act)   ref/bonsai-decoder/src/cpu_ops.cpp:199-221
   f16_*                 bd::f32_to_fp16 / fp16_to_f32
   fwht_*                bd::fwht                   ref/bonsai-decoder/src/cpu_ops.cpp:76-88
+  emb_* / emb{b}_x      the emulator's embedding lookup (src/emu_decoder.cpp:171-180:
+                        packed_code, fp16_to_f32, bd::hadamard_inverse)
+  am{i}_l / am{i}_best  bd::Sampler::argmax        ref/bonsai-decoder/src/sampler.cpp:20-25
 
 Inputs are drawn from numpy's PCG64 with fixed seeds; the fixture stores both
 inputs and outputs, so the tests never need the reference.
@@ -118,6 +121,25 @@ def main():
         out = v.copy()
         R.lib.ref_fwht(out.ctypes.data_as(__import__("ctypes").c_void_p), n)
         g[f"fwht{n}_in"], g[f"fwht{n}_out"] = v, out
+
+    # embedding lookup from a packed table (the table itself from the
+    # reference's encoder and repack), with and without the inverse transform
+    Ve, Ee = 40, 2048
+    we = (rng.standard_normal((Ve, Ee)) * (rng.random((Ve, Ee)) >= 0.3)).astype(np.float32)
+    ecodes, escales = R.repack_rows(R.quant_ptq1_0(we), Ve, Ee)
+    etoks = rng.integers(0, Ve, 5).astype(np.int32)
+    esigns = np.where(rng.random(Ee) < 0.5, -1.0, 1.0).astype(np.float32)
+    g["emb_codes"], g["emb_scales"], g["emb_toks"], g["emb_signs"] = ecodes, escales, etoks, esigns
+    for blk in (0, 128, 1024):
+        g[f"emb{blk}_x"] = R.emu_embed(ecodes, escales, etoks, Ee, Ve, blk, esigns if blk else None)
+    # greedy pick: distinct values, a tie (first index wins), -inf and all-equal rows
+    am = [rng.standard_normal(5000).astype(np.float32) for _ in range(4)]
+    am[1][[17, 4000]] = np.float32(7.5)
+    am[2][:] = -np.inf
+    am[2][[300, 301]] = np.float32(-3.0)
+    am[3][:] = np.float32(1.25)
+    for i, l in enumerate(am):
+        g[f"am{i}_l"], g[f"am{i}_best"] = l, np.int32(R.argmax(l))
 
     path = os.path.join(HERE, "golden.npz")
     np.savez_compressed(path, **g)

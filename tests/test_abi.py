@@ -96,6 +96,17 @@ def test_invalid_arguments_rejected_on_host():
     assert ex([seg, seg], 2, 1024, 1, act, None, 0, 0, act) == ARGS            # out: one segment
     assert ex([seg], 1, 1024, 1, act, None, 0, 0, h.Q8Act(0x400001, 0x500000, 0x600000)) == ARGS  # out align
     assert ex([seg], 1, 1024, 0, None, xa, 1024, 0) == h.BTF_OK                # M = 0: no-op
+    # decode-step ends: embedding lookup, greedy pick, position counter
+    tok = 0x800000
+    assert h.launch_embed_raw(codes, scales, tok, 1, 1000, None, y) == ARGS                 # E % 128
+    assert h.launch_embed_raw(codes, scales, None, 1, 1024, None, y) == ARGS                # null ids
+    assert h.launch_embed_raw(codes + 2, scales, tok, 1, 1024, None, y) == ARGS             # codes alignment
+    assert h.launch_embed_raw(codes, scales, tok, 1, 1024, h.Hx(block=96), y) == ARGS       # block not 2^k
+    assert h.launch_embed_raw(codes, scales, tok, 0, 1024, None, y) == h.BTF_OK            # M = 0: no-op
+    assert h.argmax_part_bytes(248320) >= 128 * 8
+    assert h.launch_argmax_raw(y, 0, y, tok) == ARGS                                        # empty vocabulary
+    assert h.launch_argmax_raw(y, 100, y + 4, tok) == ARGS                                  # part alignment
+    assert h.launch_argmax_raw(None, 100, y, tok) == ARGS                                   # null logits
     # step programs: every structural error is caught before the device is touched
     G = h.GemvMode
     vecs = [h.StepVec(1024, y), h.StepVec(1024, None)]

@@ -437,6 +437,101 @@ def test_gemv_fused_chain_matches_prep_chain(hip, oracle):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
 
 
+@pytest.mark.parametrize("E,block,mapped", [(1024, 0, False), (5120, 1024, False), (5120, 128, True),
+                                             (2048, 1024, False), (17408, 256, False)])
+def test_embed_bit_exact(hip, oracle, E, block, mapped):
+    """Embedding rows of a packed table (device or mapped host memory) with
+    the inverse transform equal the emulator's lookup (oracle) bit for bit;
+    tokens include the table's first and last rows."""
+    rng = np.random.default_rng(E + block)
+    V = 300
+    codes, scales = random_mat(oracle, rng, V, E)
+    toks = np.array([0, V - 1, 17, 17, 123], np.int32)
+    sg = np.where(rng.random(E) < 0.5, -1.0, 1.0).astype(np.float32) if block else None
+    ref = oracle.embed(codes, scales, toks, E, V, block, sg)
+    torch = _torch()
+    x = zeros((toks.size, E), torch.float32)
+    bufs = []
+    if mapped:
+        for a in (codes, scales):
+            b = hip.MappedHostBuffer(a.nbytes)
+            b.view()[:] = np.ascontiguousarray(a).view(np.uint8).ravel()
+            bufs.append(b)
+        cptr, sptr = bufs[0].dev, bufs[1].dev
+    else:
+        cd, sd = dev(codes), dev(scales)
+        cptr, sptr = cd, sd
+    hip.launch_embed(cptr, sptr, dev(toks), toks.size, E, hip.Hx(block=block, signs=dev(sg) if sg is not None else None),
+                     x, stream())
+    torch.cuda.synchronize()
+    got = host(x)
+    for b in bufs:
+        b.close()
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+def test_embed_block_wider_than_the_span_is_rejected(hip, oracle):
+    """As the reference launcher (src/cuda/kernels.cu:889-891): a transform
+    block must divide the span (at most 1024 columns)."""
+    rng = np.random.default_rng(5)
+    codes, scales = random_mat(oracle, rng, 8, 2048)
+    torch = _torch()
+    x = zeros((1, 2048), torch.float32)
+    with pytest.raises(RuntimeError, match="span"):
+        hip.launch_embed(dev(codes), dev(scales), dev(np.array([1], np.int32)), 1, 2048, hip.Hx(block=2048), x,
+                         stream())
+
+
+@pytest.mark.parametrize("V", [1, 100, 4097, 248320])
+def test_argmax_matches_oracle(hip, oracle, V):
+    """Greedy pick over the logits: random values, a planted tie (the smaller
+    index wins), all -inf but two, an interior NaN (never wins), all equal."""
+    rng = np.random.default_rng(V)
+    torch = _torch()
+    part = zeros((hip.argmax_part_bytes(V) // 4,), torch.int32)
+    out = zeros((1,), torch.int32)
+    cases = [rng.standard_normal(V).astype(np.float32)]
+    if V > 10:
+        t = rng.standard_normal(V).astype(np.float32)
+        t[[V // 3, V - 2]] = t.max() + 2
+        cases.append(t)
+        t = np.full(V, -np.inf, np.float32)
+        t[[5, V - 1]] = -7.0
+        cases.append(t)
+        t = rng.standard_normal(V).astype(np.float32)
+        t[V // 2] = np.nan
+        cases.append(t)
+        cases.append(np.full(V, 0.5, np.float32))
+    for l in cases:
+        hip.launch_argmax(dev(l), V, part, out, stream())
+        assert int(host(out)[0]) == oracle.argmax(l)
+
+
+def test_pos_add_eager_and_in_a_graph(hip):
+    """pos_add adds M to the device counter, eagerly and on every replay of a
+    captured graph (with eager work and syncs between the replays)."""
+    torch = _torch()
+    pos = dev(np.array([5], np.int32))
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        hip.launch_pos_add(pos, 3, s.cuda_stream)
+        s.synchronize()
+        assert int(host(pos)[0]) == 8
+        g = hip.Graph(s.cuda_stream)
+        with g:
+            hip.launch_pos_add(pos, 1, s.cuda_stream)
+        want = 8
+        for _ in range(3):
+            g.launch()
+            s.synchronize()
+            want += 1
+            assert int(host(pos)[0]) == want
+            hip.launch_pos_add(pos, 10, s.cuda_stream)
+            s.synchronize()
+            want += 10
+            assert int(host(pos)[0]) == want
+
+
 def test_graph_replay_matches_eager(hip, oracle):
     """A captured quantize + GEMV + add sequence replays identically (several
     replays with eager work and syncs between them)."""

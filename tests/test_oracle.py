@@ -359,3 +359,56 @@ def test_generator_distribution_and_determinism(oracle):
     assert np.array_equal(oracle.gen_ptq1_0(0, 3, 500, first_block=777), src[777:1277])
     assert not np.array_equal(oracle.gen_ptq1_0(0, 4, 10), src[:10])
     assert not np.array_equal(oracle.gen_ptq1_0(1, 3, 10), src[:10])
+
+
+# ---------------------------------------------------------------- either side of the chain
+@pytest.mark.parametrize("block", [0, 128, 1024])
+def test_embed_matches_fixture(oracle, golden, block):
+    E, V = 2048, 40
+    x = oracle.embed(golden["emb_codes"], golden["emb_scales"], golden["emb_toks"], E, V, block,
+                     golden["emb_signs"] if block else None)
+    assert np.array_equal(x.view(np.uint32), golden[f"emb{block}_x"].view(np.uint32))
+
+
+def test_embed_inverse_transform_round_trip(oracle, golden):
+    """The forward input transform (signs, then the normalised FWHT per block,
+    ref/bonsai-decoder/src/cpu_ops.cpp:90-111) undoes the embedding's inverse
+    one (FWHT, then signs): both factors are involutions, so the order and
+    the 1/sqrt(block) scaling are pinned."""
+    E, V = 2048, 40
+    x0 = oracle.embed(golden["emb_codes"], golden["emb_scales"], golden["emb_toks"], E, V, 0)
+    sg = golden["emb_signs"]
+    for block in (128, 1024):
+        xi = oracle.embed(golden["emb_codes"], golden["emb_scales"], golden["emb_toks"], E, V, block, sg)
+        back = np.stack([np.concatenate([oracle.fwht((r * sg)[b:b + block]) for b in range(0, E, block)]) for r in xi])
+        assert np.max(np.abs(back - x0)) <= 1e-5 * max(1.0, float(np.max(np.abs(x0))))
+        assert not np.allclose(xi, x0)
+
+
+def test_embed_rejects_token_out_of_range(oracle, golden):
+    with pytest.raises(ValueError):
+        oracle.embed(golden["emb_codes"], golden["emb_scales"], np.array([0, 40], np.int32), 2048, 40)
+
+
+def test_argmax_matches_fixture_and_numpy(oracle, golden):
+    for i in range(4):
+        l = golden[f"am{i}_l"]
+        assert oracle.argmax(l) == int(golden[f"am{i}_best"]) == int(np.argmax(l))
+
+
+def test_embed_and_argmax_vs_reference_random(oracle, ref):
+    from helpers import random_mat
+    rng = np.random.default_rng(77)
+    for E, block in [(1024, 0), (5120, 1024), (3072, 256)]:
+        V = 50
+        codes, scales = random_mat(oracle, rng, V, E)
+        toks = rng.integers(0, V, 6).astype(np.int32)
+        sg = np.where(rng.random(E) < 0.5, -1.0, 1.0).astype(np.float32) if block else None
+        a = oracle.embed(codes, scales, toks, E, V, block, sg)
+        b = ref.emu_embed(codes, scales, toks, E, V, block, sg)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    for n in (1, 7, 1000, 248320):
+        l = rng.standard_normal(n).astype(np.float32)
+        if n > 10:
+            l[[3, n - 2]] = l.max() + 1
+        assert oracle.argmax(l) == ref.argmax(l)
