@@ -36,6 +36,11 @@
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
 
+// Floating-point expressions are evaluated as written (no fused multiply-add
+// unless fmaf is spelled out), so the per-slice row sums have one defined
+// rounding order, shared by every kernel that produces them.
+#pragma clang fp contract(off)
+
 namespace btfhip {
 namespace {
 

@@ -47,6 +47,11 @@
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
 
+// Floating-point expressions are evaluated as written (no fused multiply-add
+// unless fmaf is spelled out), so the per-slice row sums have one defined
+// rounding order, shared by every kernel that produces them.
+#pragma clang fp contract(off)
+
 namespace btfhip {
 namespace {
 
@@ -123,8 +128,8 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 struct Lds {
   OpDev opd[kMaxOps];        // the program
   uint32_t act_q[2][kMaxK / 4];  // q bytes of an op's input (by op parity)
-  float act_d[2][kMaxK / 32];    // d
-  int32_t act_s[2][kMaxK / 32];  // s
+  float act_d[2][kMaxK / 32];    // d / 16
+  int32_t act_s[2][kMaxK / 32];  // -16 s
   float part[kMaxPart];       // [1024-column slice][local row]
   float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
   uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
@@ -216,9 +221,9 @@ __device__ __forceinline__ void fetch_words(const OpDev& op, Lds& L, int lane, C
         if (w < 8)
           L.act_q[ob][blk * 8 + w] = data;
         else if (w == 8)
-          L.act_d[ob][blk] = __uint_as_float(data);
+          L.act_d[ob][blk] = __uint_as_float(data) * 0.0625f;  // exact: the dot returns 16 * I
         else
-          L.act_s[ob][blk] = (int32_t)data;
+          L.act_s[ob][blk] = -16 * (int32_t)data;
       }
     }
   }
@@ -270,9 +275,9 @@ __device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t 
       if (w < 8)
         L.act_q[ob][blk * 8 + w] = data;
       else if (w == 8)
-        L.act_d[ob][blk] = __uint_as_float(data);
+        L.act_d[ob][blk] = __uint_as_float(data) * 0.0625f;
       else
-        L.act_s[ob][blk] = (int32_t)data;
+        L.act_s[ob][blk] = -16 * (int32_t)data;
     }
   }
 }
@@ -281,71 +286,49 @@ __device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t 
 typedef const __attribute__((address_space(1))) u32x4 gvec4;
 typedef const __attribute__((address_space(1))) _Float16 gf16;
 
-// The fields of an op the compute waves need, in SGPRs (read from LDS and
-// made uniform, so lane-dependent selects never become vector loads).
-struct OpR {
-  int mode, K, N, cpr, units, rot, qpu_log2, next;
-  const uint8_t* codes;
-  const uint16_t* scales;
-  const uint8_t* up_codes;
-  const uint16_t* up_scales;
-};
-__device__ __forceinline__ OpR op_r(const Lds& L, int i) {
-  const OpDev& o = L.opd[i];
-  OpR r;
-  r.mode = sgpr(o.mode);
-  r.K = sgpr(o.K);
-  r.N = sgpr(o.N);
-  r.cpr = sgpr(o.cpr);
-  r.units = sgpr(o.units);
-  r.rot = sgpr(o.rot);
-  r.qpu_log2 = sgpr(o.qpu_log2);
-  r.next = sgpr(o.next);
-  r.codes = sgpr_ptr(o.codes);
-  r.scales = sgpr_ptr(o.scales);
-  r.up_codes = sgpr_ptr(o.up_codes);
-  r.up_scales = sgpr_ptr(o.up_scales);
-  return r;
-}
-
 // Work of an op inside a workgroup: items (unit u, K-slice s, row quad q),
 // u < the workgroup's units of the op, s < S (1024-column slices), q < Qu
-// (quads of a unit: 4 rows each, or for swiglu 2 gate + 2 up rows), in the
-// order t = (u*S + s)*Qu + q: a unit's items are consecutive, so the I/O
-// waves can publish each unit as soon as it is done, and the items of a
-// compute wave touch few slices of the input. One item is one 16-byte code
-// chunk (64 columns) per lane: lane l reads chunk s*16 + (l & 15) of row
-// quad row + (l >> 4).
+// (quads of 4 rows: 8 per unit, or for swiglu 8 of the gate and 8 of the up
+// matrix), in the order t = (u*S + s)*Qu + q: a unit's items are consecutive,
+// so the I/O waves can publish each unit as soon as it is done, and the items
+// of a compute wave touch few slices of the input. One item is one 16-byte
+// code chunk (64 columns) per lane: lane l reads chunk s*16 + (l & 15) of row
+// (l >> 4) of the quad. Its partial sums land in part[s][local row] at
+// virtual row 4q + (l >> 4) of the unit (swiglu: gate row j at
+// 32*(j >> 4) + (j & 15), up row j 16 further).
 struct Slot {
   u32x4 c;
   _Float16 s;  // fp16 scale of the chunk's 128-column block
 };
 
 // The items of an op are cut into batches of kRing, and each compute wave
-// takes a contiguous run of whole batches (so only the op's last batch in
-// the workgroup is partial); a wave with no batch runs one batch of dummies,
-// which keeps every wave's ring in step across ops. Entries past n are
-// dummies (dummy load, no store).
+// takes a contiguous run of whole batches (units hold a multiple of kRing
+// items, so every batch lies in one (unit, slice) and is all real or all
+// dummy); a wave with no batch runs one batch of dummies, which keeps every
+// wave's ring in step across ops. All fields are uniform (SGPRs).
 struct OpWork {
-  int i;  // op index (>= nops: past the program's end; every entry is a dummy)
-  OpR op;
-  int S, Qu, Q, first;  // slices, quads per unit, quads of the workgroup, first unit
-  int t0, n, P;         // the wave's first item, real items, entries (a multiple of kRing)
-  int u0, s0, q0;       // (u, s, q) of item t0
+  int i;     // op index (>= nops: past the program's end; a dummy batch)
+  int next;  // the GEMV op after it
+  int S, qlog, first;  // slices, log2 quads per unit, first unit
+  int t0, n, P;        // the wave's first item, real items, entries (a multiple of kRing)
+  int u0, s0, q0;      // (u, s, q) of item t0
+  int R;               // rows of part[slice][.] (the workgroup's units x 4 * Qu)
 };
 // Every field is assigned on every path (a partly assigned struct would be
 // kept in scratch memory, whose accesses count in vmcnt).
-__device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int wg, int G, int i, const OpR& prev) {
+__device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int wg, int G, int i) {
   OpWork w;
-  const bool past = i >= nops;  // past the end: the previous op's pointers stay valid dummy addresses
+  const bool past = i >= nops;
+  const OpDev& o = L.opd[past ? 0 : i];
   w.i = i;
-  w.op = past ? prev : op_r(L, i);
-  w.first = first_unit(w.op.rot, wg, G);
-  const int nunits = past ? 0 : units_of(w.op.units, w.first, G);
-  w.S = (w.op.cpr + 15) >> 4;
-  w.Qu = 1 << w.op.qpu_log2;
-  w.Q = nunits << w.op.qpu_log2;
-  const int U = w.S << w.op.qpu_log2;  // items per unit
+  w.next = past ? nops : sgpr(o.next);
+  w.first = past ? 0 : first_unit(sgpr(o.rot), wg, G);
+  const int nunits = past ? 0 : units_of(sgpr(o.units), w.first, G);
+  w.S = past ? 1 : (sgpr(o.cpr) + 15) >> 4;
+  w.qlog = past ? 3 : sgpr(o.qpu_log2);
+  const int Qu = 1 << w.qlog;
+  w.R = (nunits << w.qlog) * 4;
+  const int U = w.S << w.qlog;  // items per unit
   const int T = nunits * U;
   // Batches are balanced over the four SIMDs, not over the waves: wave w
   // sits on SIMD w % 4, SIMDs 0 and 1 hold three compute waves and SIMDs 2
@@ -366,8 +349,8 @@ __device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int 
   w.P = (b1 > b0 ? b1 - b0 : 1) * kRing;
   const int ua = U ? w.t0 / U : 0, ra = w.t0 - ua * U;
   w.u0 = ua;
-  w.s0 = ra >> w.op.qpu_log2;
-  w.q0 = ra & (w.Qu - 1);
+  w.s0 = ra >> w.qlog;
+  w.q0 = ra & (Qu - 1);
   return w;
 }
 
@@ -376,9 +359,9 @@ __device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int 
 // from (u0, s0) to the last one's (ub, sb).
 __device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, int& b0, int& b1) {
   constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
-  const int U = w.S << w.op.qpu_log2;
+  const int U = w.S << w.qlog;
   const int tl = w.t0 + w.n - 1;
-  const int ub = tl / U, sb = (tl - ub * U) >> w.op.qpu_log2;
+  const int ub = tl / U, sb = (tl - ub * U) >> w.qlog;
   a0 = a1 = b0 = b1 = 0;
   if (ub == w.u0) {
     a0 = w.s0 * kWS, a1 = (sb + 1) * kWS;
@@ -389,59 +372,100 @@ __device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, i
   }
 }
 
-// Per-op, per-lane part of the load addresses: the lane's matrix (swiglu: odd
-// row groups read the up matrix), its row within the quad and its chunk
-// within the slice. A step program has K % 1024 == 0, so every chunk of
-// every slice is inside the row.
-struct LaneAddr {
-  uintptr_t cbase, sbase;  // codes / scales of (quad row 0, slice 0) for this lane
+// Uniform load parameters of an op. A batch covers 8 row quads of one 32-row
+// unit: for a plain op entries 0..7 read row quads 0..7 of the unit; for
+// swiglu (Qu = 16: two batches per unit and slice, 16 rows each) entries 0-3
+// read the batch's 4 row quads of the gate matrix and entries 4-7 the same
+// rows of the up matrix. So each entry reads ONE matrix, through a buffer
+// resource of that matrix (SGPRs) with the entry's uniform offset in soffset
+// and the lane's part of the offset (row in the quad, chunk in the slice) in
+// a VGPR fixed for the op: no address arithmetic on the vector ALU. A step
+// program has K % 1024 == 0, so every chunk of every slice is inside the row,
+// and every offset is below 4 GB (checked on the host); the resources span
+// 4 GB, so no access is range-clamped.
+struct OpLd {
+  __amdgpu_buffer_rsrc_t clo, chi;  // codes read by entries 0-3 / 4-7
+  __amdgpu_buffer_rsrc_t slo, shi;  // scales
+  uint32_t rowc, rows;              // bytes per row: K/4 (codes), K/64 (scales)
+  uint32_t lastc, lasts;            // offsets of the last row quad (N - 4)
+  int sw;                           // swiglu
 };
-__device__ __forceinline__ LaneAddr lane_addr(const OpR& op, int l16, int grp) {
-  LaneAddr a;
-  const bool swiglu = op.mode == BTF_GEMV_SWIGLU;
-  const bool up = swiglu && (grp & 1);
-  const int rq = swiglu ? (grp >> 1) : grp;  // row within the quad
-  const uintptr_t cm = up ? reinterpret_cast<uintptr_t>(op.up_codes) : reinterpret_cast<uintptr_t>(op.codes);
-  const uintptr_t sm = up ? reinterpret_cast<uintptr_t>(op.up_scales) : reinterpret_cast<uintptr_t>(op.scales);
-  a.cbase = cm + (size_t)rq * (op.K >> 2) + (size_t)l16 * 16;
-  a.sbase = sm + (size_t)rq * (op.K >> 6) + (size_t)(l16 >> 1) * 2;
-  return a;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
+  // stride 0, 4 GB of records, 32-bit data format (raw buffer loads)
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
+}
+__device__ __forceinline__ OpLd op_ld(const Lds& L, int i) {
+  const OpDev& o = L.opd[i];
+  OpLd d;
+  d.sw = sgpr(o.mode) == BTF_GEMV_SWIGLU;
+  const uint8_t* c = sgpr_ptr(o.codes);
+  const uint16_t* sc = sgpr_ptr(o.scales);
+  d.clo = rsrc(c);
+  d.slo = rsrc(sc);
+  d.chi = rsrc(d.sw ? sgpr_ptr(o.up_codes) : c);
+  d.shi = rsrc(d.sw ? sgpr_ptr(o.up_scales) : sc);
+  const uint32_t K = (uint32_t)sgpr(o.K), N = (uint32_t)sgpr(o.N);
+  d.rowc = K >> 2;
+  d.rows = K >> 6;
+  d.lastc = (N - 4) * d.rowc;
+  d.lasts = (N - 4) * d.rows;
+  return d;
+}
+// This lane's part of an entry's offsets: row grp of the quad, chunk l16 of
+// the slice (16 code bytes; the fp16 scale of its 128-column block).
+struct LaneOff {
+  uint32_t c, s;
+};
+__device__ __forceinline__ LaneOff lane_off(const OpLd& d, int l16, int grp) {
+  return LaneOff{(uint32_t)grp * d.rowc + (uint32_t)l16 * 16u, (uint32_t)grp * d.rows + (uint32_t)(l16 >> 1) * 2u};
 }
 
-// (u, s, q) cursor advanced without divisions.
-struct Cur {
-  int u, s, q;
+// Position of a batch in the op's items: local unit, slice, first quad.
+struct BPos {
+  int u, s, qb;
 };
-__device__ __forceinline__ void cur_next(int Qu, int S, Cur& c) {
-  if (++c.q == Qu) {
-    c.q = 0;
-    if (++c.s == S) {
-      c.s = 0;
-      ++c.u;
+__device__ __forceinline__ void bpos_next(int qlog, int S, BPos& p) {
+  p.qb += kRing;
+  if (p.qb == (1 << qlog)) {
+    p.qb = 0;
+    if (++p.s == S) {
+      p.s = 0;
+      ++p.u;
     }
   }
 }
-
-// Load item (u, s, q) into a ring slot, or (real == false) the lane's chunk of
-// the op's first quad and slice, so every refill is an unconditional load
-// into the slot's own registers. The item's offset is uniform (SGPRs); quads
-// past N (N % 4 == 0, swiglu N % 2 == 0: a quad is all in or all out) read
-// quad 0.
-__device__ __forceinline__ void issue_item(const OpR& op, const LaneAddr& la, int first, const Cur& c, bool real,
-                                           int G, Slot& sl) {
-  int row0 = (first + c.u * G) * 32 + (op.mode == BTF_GEMV_SWIGLU ? 2 * c.q : 4 * c.q);
-  row0 = real && row0 < op.N ? row0 : 0;
-  const int s = real ? c.s : 0;
-  // 32-bit uniform offsets (a matrix is below 4 GB, checked on the host)
-  const uint32_t co = (uint32_t)row0 * (uint32_t)(op.K >> 2) + (uint32_t)s * 256u;
-  const uint32_t so = (uint32_t)row0 * (uint32_t)(op.K >> 6) + (uint32_t)s * 16u;
-  sl.c = __builtin_nontemporal_load(reinterpret_cast<gvec4*>(la.cbase + co));
-  sl.s = __builtin_nontemporal_load(reinterpret_cast<gf16*>(la.sbase + so));
+// Uniform offsets of a batch's entry 0 and the largest valid ones (the last
+// row quad's chunk of the same slice).
+struct BAddr {
+  uint32_t oc, os, mc, ms;
+};
+__device__ __forceinline__ BAddr batch_addr(const OpLd& d, int first, int G, const BPos& p) {
+  const uint32_t row = (uint32_t)(first + p.u * G) * 32u + ((uint32_t)p.qb << (d.sw ? 1 : 2));
+  BAddr a;
+  a.oc = row * d.rowc + (uint32_t)p.s * 256u;
+  a.os = row * d.rows + (uint32_t)p.s * 16u;
+  a.mc = d.lastc + (uint32_t)p.s * 256u;
+  a.ms = d.lasts + (uint32_t)p.s * 16u;
+  return a;
+}
+// Load entry r of a batch into its ring slot: an unconditional load pair into
+// the slot's own registers (non-temporal: the weights are read once). Rows
+// past N (only in an op's last unit; N % 4 == 0: a quad is all in or all out)
+// and dummy batches read the last row quad instead (never stored).
+constexpr int kNT = 2;  // cache policy: non-temporal
+__device__ __forceinline__ void issue_entry(const OpLd& d, const LaneOff& lo, const BAddr& a, int r, Slot& sl) {
+  const bool hi = r >= 4;
+  const uint32_t dr = 4u * (uint32_t)(r & 3) + (hi && !d.sw ? 16u : 0u);  // rows past the batch's first
+  const uint32_t oc = min(a.oc + dr * d.rowc, a.mc);
+  const uint32_t os = min(a.os + dr * d.rows, a.ms);
+  sl.c = __builtin_amdgcn_raw_buffer_load_b128(hi ? d.chi : d.clo, (int)lo.c, (int)oc, kNT);
+  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(hi ? d.shi : d.slo, (int)lo.s, (int)os, kNT);
+  __builtin_memcpy(&sl.s, &h, 2);
 }
 
-// The activation of this lane's chunk of slice s (64 q bytes, d/16, -s of
-// its two sub-blocks). The 4 row groups of a wave read the same addresses
-// (LDS broadcasts).
+// The activation of this lane's chunk of slice s: 64 q bytes, and per
+// sub-block d/16 and -16 s (stored so by the input fetch). The 4 row groups of a
+// wave read the same addresses (LDS broadcasts).
 __device__ __forceinline__ void load_act(const Lds& L, int ob, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
                                          int (&an)[2]) {
   const int chunk = s * 16 + l16;
@@ -456,98 +480,130 @@ __device__ __forceinline__ void load_act(const Lds& L, int ob, int s, int l16, u
   }
   const float2 d = *reinterpret_cast<const float2*>(&L.act_d[ob][2 * chunk]);
   const int2 sv = *reinterpret_cast<const int2*>(&L.act_s[ob][2 * chunk]);
-  ad[0] = d.x * 0.0625f;  // exact: the dot returns 16 * I
-  ad[1] = d.y * 0.0625f;
-  an[0] = -sv.x;
-  an[1] = -sv.y;
+  ad[0] = d.x;
+  ad[1] = d.y;
+  an[0] = sv.x;
+  an[1] = sv.y;
 }
 
-// dot4 with a zero accumulator in one VOP3P instruction (the builtin with a
-// constant 0 becomes a register clear plus the two-operand form).
-__device__ __forceinline__ int sdot4_0(uint32_t a, uint32_t b) {
-  int r;
-  asm("v_dot4_i32_i8 %0, %1, %2, 0" : "=v"(r) : "v"(a), "v"(b));
-  return r;
-}
-// subblock_dot16 (common.h) with the zero-started chains in VOP3P form; the
-// same integer result.
-__device__ __forceinline__ int subblock_dot16_z(uint32_t w0, uint32_t w1, const uint32_t* a, int ns) {
-  int c0 = sdot4(w0 & 0x03030303u, a[0], ns);
-  c0 = sdot4(w1 & 0x03030303u, a[4], c0);
-  int c1 = sdot4_0(w0 & 0x0C0C0C0Cu, a[1]);
-  c1 = sdot4(w1 & 0x0C0C0C0Cu, a[5], c1);
-  int c2 = sdot4_0(w0 & 0x30303030u, a[2]);
-  c2 = sdot4((w0 >> 2) & 0x30303030u, a[3], c2);
-  c2 = sdot4(w1 & 0x30303030u, a[6], c2);
-  c2 = sdot4((w1 >> 2) & 0x30303030u, a[7], c2);
-  return (((c0 << 2) + c1) << 2) + c2;
+// 16 * (code . q - s) over the two 32-column sub-blocks of a 16-byte chunk,
+// as subblock_dot16 (common.h): the same masks, and the partial sums
+// recombined as 16*c0 + 4*c1 + c23, but each chain starts from the previous
+// one shifted (c1 from c0 << 2, c23 from (c1 << 2) - 16 s), so every dot but
+// the first accumulates into a dead register (the two-operand form, no
+// copies). The first has a zero accumulator and the clamp bit, which keeps
+// it in the three-operand form (no register clear; the sums are far from
+// saturating: |result| < 2^18). The two sub-blocks' chains are interleaved so
+// that no instruction waits on the one just before it. ns16 = -16 s.
+__device__ __forceinline__ void chunk_dot16(const u32x4& w, const uint32_t (&a)[16], const int (&ns16)[2], int& y0,
+                                            int& y1) {
+  int c = __builtin_amdgcn_sdot4((int)(w.x & 0x03030303u), (int)a[0], 0, true);
+  int e = __builtin_amdgcn_sdot4((int)(w.z & 0x03030303u), (int)a[8], 0, true);
+  c = sdot4(w.y & 0x03030303u, a[4], c);
+  e = sdot4(w.w & 0x03030303u, a[12], e);
+  c = sdot4(w.x & 0x0C0C0C0Cu, a[1], c << 2);
+  e = sdot4(w.z & 0x0C0C0C0Cu, a[9], e << 2);
+  c = sdot4(w.y & 0x0C0C0C0Cu, a[5], c);
+  e = sdot4(w.w & 0x0C0C0C0Cu, a[13], e);
+  c = sdot4(w.x & 0x30303030u, a[2], (c << 2) + ns16[0]);
+  e = sdot4(w.z & 0x30303030u, a[10], (e << 2) + ns16[1]);
+  c = sdot4((w.x >> 2) & 0x30303030u, a[3], c);
+  e = sdot4((w.z >> 2) & 0x30303030u, a[11], e);
+  c = sdot4(w.y & 0x30303030u, a[6], c);
+  e = sdot4(w.w & 0x30303030u, a[14], e);
+  c = sdot4((w.y >> 2) & 0x30303030u, a[7], c);
+  e = sdot4((w.w >> 2) & 0x30303030u, a[15], e);
+  y0 = c;
+  y1 = e;
 }
 
-// One consumed entry: the dot products of ring slot `sl` (read before the
-// slot is refilled), then the refill.
+// One consumed entry: the dot products and the scale of ring slot `sl`,
+// taken before the slot is refilled (the empty asm pins them there, so they
+// are neither sunk past the refill nor folded into a later v_fma_mix).
 struct Consumed {
   int y0, y1;
   float f;
 };
 __device__ __forceinline__ Consumed consume(const Slot& sl, const uint32_t (&aq)[16], const int (&an)[2]) {
-  // The empty asm keeps the fp16 -> f32 conversion from being folded into a
-  // later v_fma_mix that would read the slot after the refill.
   Consumed r;
   const u32x4 wv = sl.c;
   r.f = (float)sl.s;
-  asm volatile("" : "+v"(r.f));
-  r.y0 = subblock_dot16_z(wv.x, wv.y, &aq[0], an[0]);
-  r.y1 = subblock_dot16_z(wv.z, wv.w, &aq[8], an[1]);
+  chunk_dot16(wv, aq, an, r.y0, r.y1);
+  asm volatile("" : "+v"(r.f), "+v"(r.y0), "+v"(r.y1));
   return r;
 }
-// Finish an entry: scale, 16-lane DPP reduction, store of the slice's
-// partial sum of the row into LDS part[s][local row], then the wave's count
-// of done items of the unit (a plain store of a uniform value: LDS
-// operations of a wave complete in order, so the I/O waves see the partial
-// sums once they see the count).
-__device__ __forceinline__ void finish(const Consumed& c, const float (&ad)[2], bool store, int part_idx,
-                                       uint32_t* count, uint32_t done, int lane, Lds& L) {
-  float p = ad[0] * (float)c.y0;
-  p = fmaf(ad[1], (float)c.y1, p);
-  float acc = c.f * p;
-  acc = row16_sum(acc);
-  if (store) {
-    if ((lane & 15) == 0) L.part[part_idx] = acc;
-    asm volatile("" ::: "memory");
-    *count = done;
+
+// The 16-lane row sums of a batch's 8 entry values, each in the addition
+// tree of row16_sum (partners across lane bit 0, then 1, 2, 3; the same
+// floating-point result), for all 8 at once: the first two levels also sort
+// the entries over the lanes (lane l keeps entry l & 3 in z0, entry
+// 4 + (l & 3) in z1); the last two are row rotations by 4 and 8. A rotation
+// by 8 pairs every lane with its exact bit-3 partner l ^ 8; a rotation by 4
+// brings lane l ^ 4 to half of the lanes (those with bit 2 clear or those
+// with it set, by the rotation's direction), and there the sums are exact:
+// sum_lanes() names them.
+__device__ __forceinline__ void reduce8(const float (&v)[kRing], bool b0, bool b1, float& z0, float& z1) {
+  float w[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const float keep = b0 ? v[2 * k + 1] : v[2 * k];
+    const float send = b0 ? v[2 * k] : v[2 * k + 1];
+    w[k] = keep + dpp_f<0xB1>(send);  // quad_perm(1,0,3,2): lane l ^ 1
   }
+  float x[2];
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const float keep = b1 ? w[2 * k + 1] : w[2 * k];
+    const float send = b1 ? w[2 * k] : w[2 * k + 1];
+    x[k] = keep + dpp_f<0x4E>(send);  // quad_perm(2,3,0,1): lane l ^ 2
+  }
+  z0 = x[0] + dpp_f<0x124>(x[0]);  // row_ror:4
+  z1 = x[1] + dpp_f<0x124>(x[1]);
+  z0 = z0 + dpp_f<0x128>(z0);      // row_ror:8
+  z1 = z1 + dpp_f<0x128>(z1);
+}
+// Lanes 0-7 of a row whose row_ror:4 source is their bit-2 partner: 4 lanes
+// per row, holding reduce8's sums of entries (l & 3) and 4 + (l & 3).
+__device__ __forceinline__ bool sum_lanes(int l16) {
+  return l16 < 8 && dpp_i<0x124>(l16) == (l16 ^ 4);
 }
 
 // The compute waves' whole program. Per op: wait for the input slices the
 // wave's items read (fetch them, or for an early op wait until the I/O waves
 // have), the op's batches of kRing entries, barrier B (every wave done with
-// the op). Entry e of the op lives in ring slot e % kRing; consuming it
-// refills the slot with entry e + kRing of the op, and in the op's last
-// batch (a separate copy of the loop body) with entry e + kRing - P of the
-// NEXT op: the ring stays full across op boundaries (the next op's first
-// loads are in flight while this op finishes and while the wave waits for
-// its input), with no dummy loads to drain. Each copy of the body is
+// the op). Entry r of a batch lives in ring slot r; consuming it refills the
+// slot with entry r of the next batch, which for the op's last batch is the
+// NEXT op's first batch: the ring stays full across op boundaries (the next
+// op's first loads are in flight while this op finishes and while the wave
+// waits for its input), with no dummy loads to drain. The loop body is
 // straight-line code with one unconditional load pair per entry, so the
-// compiler keeps each slot in fixed registers with exact wait counts. The
-// activation stays in registers and is reloaded from LDS when the slice
-// changes.
+// compiler keeps each slot in fixed registers with exact wait counts; the
+// per-batch bookkeeping (addresses, partial-sum slots, the unit's count, the
+// activation reload at a new slice) is uniform and done once per batch.
 __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
                                               uint32_t base_tag) {
   const int l16 = lane & 15, grp = lane >> 4;
+  const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
+  const bool sum_lane = sum_lanes(l16);
   Slot ring[kRing];
-  OpWork cur = op_work(L, nops, wave, wg, G, first, op_r(L, first));
-  OpWork nxt = op_work(L, nops, wave, wg, G, cur.op.next, cur.op);
-  LaneAddr la_cur = lane_addr(cur.op, l16, grp);
-  LaneAddr la_nxt = lane_addr(nxt.op, l16, grp);
+  OpWork cur = op_work(L, nops, wave, wg, G, first);
+  OpLd ld_cur = op_ld(L, first);
+  LaneOff lo_cur = lane_off(ld_cur, l16, grp);
   {
-    Cur c{cur.u0, cur.s0, cur.q0};
+    const BAddr a = batch_addr(ld_cur, cur.first, G, BPos{cur.u0, cur.s0, cur.q0});
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) {
-      issue_item(cur.op, la_cur, cur.first, c, r < cur.n, G, ring[r]);
-      cur_next(cur.Qu, cur.S, c);
-    }
+    for (int r = 0; r < kRing; ++r) issue_entry(ld_cur, lo_cur, a, r, ring[r]);
   }
   for (;;) {
+    // the next op's first batch (past the program's end: this op's matrices)
+    OpLd ld_nxt = ld_cur;
+    BAddr a_nxt;
+    {
+      const OpWork nw = op_work(L, nops, wave, wg, G, cur.next);
+      if (cur.next < nops) ld_nxt = op_ld(L, cur.next);
+      a_nxt = batch_addr(ld_nxt, nw.first, G, BPos{nw.u0, nw.s0, nw.q0});
+    }
+    const LaneOff lo_nxt = lane_off(ld_nxt, l16, grp);
     const int ob = cur.i & 1;  // LDS buffers of this op
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
@@ -563,70 +619,61 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
         }
         asm volatile("" ::: "memory");
       } else {
-        int a0, a1, b0, b1;
-        input_words(cur, a0, a1, b0, b1);
-        fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0, b1);
+        int a0, a1, b0w, b1w;
+        input_words(cur, a0, a1, b0w, b1w);
+        fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0w, b1w);
         // the words other lanes of this wave wrote are read below
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
     }
-    const int R = cur.Q * 4;  // rows (virtual: swiglu gate/up interleaved) of this workgroup
-    const int U = cur.S << cur.op.qpu_log2;  // items per unit
-    Cur cc{cur.u0, cur.s0, cur.q0};  // entry being consumed
-    Cur lc = cc;                     // entry being loaded (kRing ahead)
-#pragma unroll
-    for (int r = 0; r < kRing; ++r) cur_next(cur.Qu, cur.S, lc);
+    const int U = cur.S << cur.qlog;  // items per unit
+    BPos cp{cur.u0, cur.s0, cur.q0};  // the batch being consumed
     uint32_t aq[16];
     float ad[2];
     int an[2];
-    load_act(L, ob, cc.s, l16, aq, ad, an);
+    load_act(L, ob, cp.s, l16, aq, ad, an);
     const int nb = cur.P / kRing;
-    for (int b = 0; b < nb - 1; ++b) {
+    for (int b = 0; b < nb; ++b) {
+      // refills: the next batch of this op, or in the last batch the next op's first
+      BPos np = cp;
+      bpos_next(cur.qlog, cur.S, np);
+      const bool last = b == nb - 1;
+      const OpLd& ld = last ? ld_nxt : ld_cur;
+      const LaneOff lo = last ? lo_nxt : lo_cur;
+      const BAddr a = last ? a_nxt : batch_addr(ld_cur, cur.first, G, np);
+      float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
-        const int e = b * kRing + r;
         const Consumed c = consume(ring[r], aq, an);
         __builtin_amdgcn_sched_barrier(0);
-        issue_item(cur.op, la_cur, cur.first, lc, e + kRing < cur.n, G, ring[r]);
+        issue_entry(ld, lo, a, r, ring[r]);
         __builtin_amdgcn_sched_barrier(0);
-        cur_next(cur.Qu, cur.S, lc);
-        finish(c, ad, e < cur.n, cc.s * R + ((cc.u << cur.op.qpu_log2) + cc.q) * 4 + grp, &L.ucnt[wave][cc.u],
-               (uint32_t)(cur.t0 + e + 1 - max(cur.t0, cc.u * U)), lane, L);
-        const int s_prev = cc.s;
-        cur_next(cur.Qu, cur.S, cc);
-        if (cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
+        float p = ad[0] * (float)c.y0;
+        p = fmaf(ad[1], (float)c.y1, p);
+        v[r] = c.f * p;
       }
-    }
-    if (cur.n == 0) {  // no real entry: only the refills with the next op's first entries
-      Cur ln{nxt.u0, nxt.s0, nxt.q0};
-#pragma unroll
-      for (int r = 0; r < kRing; ++r) {
-        issue_item(nxt.op, la_nxt, nxt.first, ln, r < nxt.n, G, ring[r]);
-        cur_next(nxt.Qu, nxt.S, ln);
+      float z0, z1;
+      reduce8(v, b0, b1, z0, z1);
+      if (b * kRing < cur.n) {  // a real batch: its partial sums into part[slice][local row]
+        const int pb = cp.s * cur.R + (((cp.u << cur.qlog) + cp.qb) << 2) + grp;
+        if (sum_lane) {
+          L.part[pb + 4 * (l16 & 3)] = z0;
+          L.part[pb + 4 * (l16 & 3) + 16] = z1;
+        }
+        // then the wave's count of done items of the unit (a plain store of a
+        // uniform value: LDS operations of a wave complete in order, so the
+        // I/O waves see the partial sums once they see the count)
+        asm volatile("" ::: "memory");
+        L.ucnt[wave][cp.u] = (uint32_t)(cur.t0 + (b + 1) * kRing - max(cur.t0, cp.u * U));
       }
-    } else {  // last batch: the refills load the next op's first entries
-      Cur ln{nxt.u0, nxt.s0, nxt.q0};
-#pragma unroll
-      for (int r = 0; r < kRing; ++r) {
-        const int e = cur.P - kRing + r;
-        const Consumed c = consume(ring[r], aq, an);
-        __builtin_amdgcn_sched_barrier(0);
-        issue_item(nxt.op, la_nxt, nxt.first, ln, r < nxt.n, G, ring[r]);
-        __builtin_amdgcn_sched_barrier(0);
-        cur_next(nxt.Qu, nxt.S, ln);
-        finish(c, ad, e < cur.n, cc.s * R + ((cc.u << cur.op.qpu_log2) + cc.q) * 4 + grp, &L.ucnt[wave][cc.u],
-               (uint32_t)(cur.t0 + e + 1 - max(cur.t0, cc.u * U)), lane, L);
-        const int s_prev = cc.s;
-        cur_next(cur.Qu, cur.S, cc);
-        if (r + 1 < kRing && cc.s != s_prev) load_act(L, ob, cc.s, l16, aq, ad, an);
-      }
+      if (!last && np.s != cp.s) load_act(L, ob, np.s, l16, aq, ad, an);
+      cp = np;
     }
     lds_barrier();  // B: every wave is done with the op
-    if (nxt.i >= nops) break;
-    cur = nxt;
-    la_cur = la_nxt;
-    nxt = op_work(L, nops, wave, wg, G, cur.op.next, cur.op);
-    la_nxt = lane_addr(nxt.op, l16, grp);
+    if (cur.next >= nops) break;
+    cur = op_work(L, nops, wave, wg, G, cur.next);
+    ld_cur = ld_nxt;
+    lo_cur = lo_nxt;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the trailing dummy loads
 }
@@ -733,11 +780,11 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
     const bool valid = row < N;
     float v;
     if (mode == BTF_GEMV_SWIGLU) {
-      const int lr = ui * 64 + 2 * j;  // virtual rows: gate 2j, up 2j+1 of this unit
+      const int lr = ui * 64 + 32 * (j >> 4) + (j & 15);  // virtual rows: gate row j; up row j at lr + 16
       float g = 0.f, u = 0.f;
       for (int s = 0; s < S; ++s) {
         g += L.part[s * R + lr];
-        u += L.part[s * R + lr + 1];
+        u += L.part[s * R + lr + 16];
       }
       v = g / (1.0f + expf(-g)) * u;
     } else {
