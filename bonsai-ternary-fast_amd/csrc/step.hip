@@ -249,8 +249,11 @@ __device__ __forceinline__ void early_issue(const OpDev& op, int lid, uint32_t b
     f.v[b] = idx < nin ? ll_load(in + idx) : ((uint64_t)tin << 32);
   }
 }
-__device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, Lds& L, int ob,
-                                             Ctl* ctl) {
+// Polls what was stale, writes the input into LDS buffer `ob`, then this
+// wave's L.early_seq = seq. Returns false (and writes nothing) if `wait` is
+// false and some word of this wave is not yet published.
+__device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, Lds& L, int ob,
+                                             Ctl* ctl, bool wait, uint32_t seq) {
   const uint64_t* in = sgpr_ptr(op.in_q8);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
@@ -259,7 +262,8 @@ __device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t 
     uint32_t pending = 0;
 #pragma unroll
     for (int b = 0; b < kEIn; ++b) pending |= ((uint32_t)(f.v[b] >> 32) != tin) ? (1u << b) : 0u;
-    if (pending == 0) break;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+    if (!wait) return false;
     if (!poll_step(spins, L, ctl)) break;
     for (int b = 0; b < kEIn; ++b) {
       const int idx = lid + b * kIL;
@@ -280,6 +284,9 @@ __device__ __forceinline__ void early_finish(const OpDev& op, int lid, uint32_t 
         L.act_s[ob][blk] = -16 * (int32_t)data;
     }
   }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the input words are in LDS
+  if ((lid & 63) == 0) __hip_atomic_store(&L.early_seq[lid >> 6], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  return true;
 }
 
 // ---------------------------------------------------------------- compute waves
@@ -607,13 +614,15 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     const int ob = cur.i & 1;  // LDS buffers of this op
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
-        // fetched by the I/O waves after the previous op's barrier B
+        // fetched by the I/O waves (early_seq only grows within a launch:
+        // they may have gone on to fetch the next early op's input, into
+        // the other buffer)
         uint32_t spins = 0;
         for (;;) {
           bool ready = true;
 #pragma unroll
           for (int k = 0; k < kIW; ++k)
-            ready &= __hip_atomic_load(&L.early_seq[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) ==
+            ready &= __hip_atomic_load(&L.early_seq[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
                      (uint32_t)cur.i + 1;
           if (ready || !poll_step(spins, L, ctl)) break;
         }
@@ -826,18 +835,19 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     const int nx = sgpr(op.next);
     const bool early = nx < nops && sgpr(L.opd[nx].early);
     EarlyFetch ef;
+    bool early_done = !early;
     if (early) early_issue(L.opd[nx], iol, base_tag, ef);
     wait_readers(sgpr(op.war_op), rd_cnt, G, L, ctl);
+    // Finish the early fetch now if its input is all published (usual: its
+    // producers are two or more ops back), while this op's first units are
+    // still being computed. Waiting for these loads later would also wait
+    // for the op's own output stores to complete (vmcnt counts both).
+    if (early) early_done = early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, false, (uint32_t)nx + 1);
     io_publish(op, L, wg, G, iol, base_tag, ctl);
     lds_barrier();  // B: every compute wave is done with the op's input
     if (sgpr(op.count_reads) && iol == 0)
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (early) {
-      early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl);
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the input words are in LDS
-      if ((iol & 63) == 0)
-        __hip_atomic_store(&L.early_seq[iol >> 6], (uint32_t)nx + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-    }
+    if (!early_done) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, true, (uint32_t)nx + 1);
   }
 }
 
