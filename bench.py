@@ -538,8 +538,11 @@ def main():
     except (OSError, ValueError):
         traffic_tab = {}
     if engine == "step":
+        tr = traffic_tab.get("step/step_kernel") if step.M == 1 and args.workload == "sweep" and \
+            layers == LAYERS else None
         roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": None,
+                "frac": round(value / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
+                "traffic_source": tr["source"] if tr else None,
                 "kernel": "step_kernel (the whole GEMV chain, one launch per step)",
                 "bytes_per_launch": step.total_bytes, "avg_launch_us": round(ms * 1e3, 3)}
     else:
