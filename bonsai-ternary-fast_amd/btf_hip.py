@@ -60,6 +60,27 @@ class _DeviceInfo(C.Structure):
                 ("total_mem_bytes", C.c_int64), ("name", C.c_char * 256), ("gcn_arch", C.c_char * 64)]
 
 
+class _GgufHeader(C.Structure):
+    _fields_ = [("version", C.c_uint32), ("alignment", C.c_uint64), ("data_offset", C.c_uint64),
+                ("file_bytes", C.c_uint64), ("n_tensors", C.c_int64), ("n_kv", C.c_int64)]
+
+
+class _GgufTensor(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_int), ("ne", C.c_int64 * 4), ("type", C.c_uint32),
+                ("offset", C.c_uint64), ("bytes", C.c_uint64), ("data", C.c_void_p)]
+
+
+class _GgufKv(C.Structure):
+    _fields_ = [("key", C.c_void_p), ("key_len", C.c_uint64), ("type", C.c_uint32), ("arr_type", C.c_uint32),
+                ("len", C.c_uint64)]
+
+
+class _PackPlan(C.Structure):
+    _fields_ = [("n_matrices", C.c_int64), ("codes_bytes", C.c_uint64), ("scales_bytes", C.c_uint64),
+                ("arena_bytes", C.c_uint64), ("source_bytes", C.c_uint64), ("other_bytes", C.c_uint64),
+                ("staging_host_bytes", C.c_uint64), ("staging_device_bytes", C.c_uint64)]
+
+
 def _decl(name, args, res=C.c_int):
     f = getattr(_lib, name)
     f.argtypes = args
@@ -101,6 +122,21 @@ _step_launch = _decl("btf_hip_step_launch", [_vp, _vp])
 _step_error = _decl("btf_hip_step_error", [_vp, C.POINTER(C.c_int)])
 _step_destroy = _decl("btf_hip_step_destroy", [_vp])
 _step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
+_gguf_open = _decl("btf_hip_gguf_open", [C.c_char_p, _i, C.POINTER(C.c_void_p)])
+_gguf_close = _decl("btf_hip_gguf_close", [_vp])
+_gguf_info = _decl("btf_hip_gguf_info", [_vp, C.POINTER(_GgufHeader)])
+_gguf_tensor = _decl("btf_hip_gguf_tensor", [_vp, _i64, C.POINTER(_GgufTensor)])
+_gguf_find_tensor = _decl("btf_hip_gguf_find_tensor", [_vp, C.c_char_p], _i64)
+_gguf_kv = _decl("btf_hip_gguf_kv", [_vp, _i64, C.POINTER(_GgufKv)])
+_gguf_find_kv = _decl("btf_hip_gguf_find_kv", [_vp, C.c_char_p], _i64)
+_gguf_kv_num = _decl("btf_hip_gguf_kv_num", [_vp, _i64, C.c_uint64, C.POINTER(C.c_int64), C.POINTER(C.c_double)])
+_gguf_kv_str = _decl("btf_hip_gguf_kv_str", [_vp, _i64, C.c_uint64, C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)])
+_ggml_row_bytes = _decl("btf_hip_ggml_row_bytes", [C.c_uint32, _i64], _i64)
+_gguf_plan = _decl("btf_hip_gguf_plan", [_vp, C.c_uint64, C.POINTER(_PackPlan)])
+_loader_create = _decl("btf_hip_loader_create", [C.c_uint64, C.POINTER(C.c_void_p)])
+_loader_upload = _decl("btf_hip_loader_upload_ptq1_0", [_vp, _vp, _i64, _i64, _vp, _vp, _vp])
+_loader_finish = _decl("btf_hip_loader_finish", [_vp, C.POINTER(C.c_uint64)])
+_loader_destroy = _decl("btf_hip_loader_destroy", [_vp])
 
 #: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
 ABI_SYMBOLS = (
@@ -113,7 +149,11 @@ ABI_SYMBOLS = (
     "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
     "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
     "btf_hip_graph_destroy", "btf_hip_step_create", "btf_hip_step_launch", "btf_hip_step_error",
-    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit",
+    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_gguf_open", "btf_hip_gguf_close",
+    "btf_hip_gguf_info", "btf_hip_gguf_tensor", "btf_hip_gguf_find_tensor", "btf_hip_gguf_kv",
+    "btf_hip_gguf_find_kv", "btf_hip_gguf_kv_num", "btf_hip_gguf_kv_str", "btf_hip_ggml_row_bytes",
+    "btf_hip_gguf_plan", "btf_hip_loader_create", "btf_hip_loader_upload_ptq1_0", "btf_hip_loader_finish",
+    "btf_hip_loader_destroy",
 )
 
 
@@ -445,6 +485,177 @@ class MappedHostBuffer:
 
     def __del__(self):
         self.close()
+
+
+GGUF_STRING, GGUF_ARRAY, GGUF_F32, GGUF_F64 = 8, 9, 6, 12
+GGML_PTQ1_0 = 143
+
+
+@dataclass
+class GgufTensorInfo:
+    name: str
+    n_dims: int
+    ne: tuple
+    type: int
+    offset: int
+    bytes: int
+    data: int | None  # host address inside the mapping (None: past the end of a header-only read)
+
+
+class Gguf:
+    """A GGUF v2/v3 file, memory-mapped (btf_hip_gguf_*): the reference's
+    bd::Gguf interface (ref/bonsai-decoder/include/bd/gguf.hpp:49-85) over the
+    C ABI. Raises RuntimeError with the reader's reason on a bad file."""
+
+    def __init__(self, path: str, header_only: bool = False):
+        h = C.c_void_p()
+        _check(_gguf_open(os.fsencode(path), int(header_only), C.byref(h)))
+        self.h = h.value
+        hd = _GgufHeader()
+        _check(_gguf_info(self.h, C.byref(hd)))
+        self.version, self.alignment, self.data_offset = hd.version, hd.alignment, hd.data_offset
+        self.file_bytes, self.n_tensors, self.n_kv = hd.file_bytes, hd.n_tensors, hd.n_kv
+
+    def tensor_info(self, index: int) -> GgufTensorInfo:
+        t = _GgufTensor()
+        _check(_gguf_tensor(self.h, index, C.byref(t)))
+        return GgufTensorInfo(t.name.decode("utf-8", "surrogateescape"), t.n_dims, tuple(t.ne[:t.n_dims]), t.type,
+                              t.offset, t.bytes, t.data)
+
+    @property
+    def tensors(self):
+        return [self.tensor_info(i) for i in range(self.n_tensors)]
+
+    def tensor(self, name: str) -> GgufTensorInfo | None:
+        i = _gguf_find_tensor(self.h, name.encode())
+        return None if i < 0 else self.tensor_info(i)
+
+    def kv_entry(self, index: int):
+        """(key bytes, type, arr_type, values): numbers as (int, float)
+        pairs, strings as bytes; a scalar's values hold one element."""
+        k = _GgufKv()
+        _check(_gguf_kv(self.h, index, C.byref(k)))
+        key = C.string_at(k.key, k.key_len)
+        et = k.arr_type if k.type == GGUF_ARRAY else k.type
+        vals = []
+        for e in range(k.len):
+            if et == GGUF_STRING:
+                sp, n = C.c_void_p(), C.c_uint64()
+                _check(_gguf_kv_str(self.h, index, e, C.byref(sp), C.byref(n)))
+                vals.append(C.string_at(sp.value, n.value) if n.value else b"")
+            else:
+                iv, fv = C.c_int64(), C.c_double()
+                _check(_gguf_kv_num(self.h, index, e, C.byref(iv), C.byref(fv)))
+                vals.append((iv.value, fv.value))
+        return key, k.type, k.arr_type, vals
+
+    def get(self, key: str, default=None):
+        """A metadata value: int/float/str for a scalar, a list for an array."""
+        i = _gguf_find_kv(self.h, key.encode())
+        if i < 0:
+            return default
+        _, t, at, vals = self.kv_entry(i)
+        conv = (lambda v: v.decode("utf-8", "surrogateescape")) if (at if t == GGUF_ARRAY else t) == GGUF_STRING \
+            else (lambda v: v[1]) if (at if t == GGUF_ARRAY else t) in (GGUF_F32, GGUF_F64) else (lambda v: v[0])
+        return [conv(v) for v in vals] if t == GGUF_ARRAY else conv(vals[0])
+
+    def dump(self) -> str:
+        """Canonical text of everything parsed (the format of the oracle's
+        reference-reader dump: strings as length:hex, numbers as int and
+        %.17g)."""
+        def hx(b):
+            return f"{len(b)}:{b.hex()}"
+
+        def num(f):
+            return ("%.17g" % f) if f == f else ("-nan" if str(f).startswith("-") else "nan")
+        out = [f"version {self.version}", f"alignment {self.alignment}", f"data_offset {self.data_offset}",
+               f"n_tensors {self.n_tensors}", f"n_kv {self.n_kv}"]
+        for i in range(self.n_kv):
+            key, t, at, vals = self.kv_entry(i)
+            line = f"kv {hx(key)} {t}"
+            if t == GGUF_ARRAY:
+                line += f" {at} {len(vals)}"
+                for v in vals:
+                    line += " " + (hx(v) if at == GGUF_STRING else num(v[1]) if at in (GGUF_F32, GGUF_F64)
+                                   else str(v[0]))
+            elif t == GGUF_STRING:
+                line += " " + hx(vals[0])
+            else:
+                line += f" {vals[0][0]} {num(vals[0][1])}"
+            out.append(line)
+        for i in range(self.n_tensors):
+            t = _GgufTensor()
+            _check(_gguf_tensor(self.h, i, C.byref(t)))
+            out.append(f"tensor {hx(t.name)} {t.type} {t.n_dims} " + " ".join(str(x) for x in t.ne[:t.n_dims]) +
+                       f" {t.offset} {t.bytes} {1 if t.data else 0}")
+        return "\n".join(out) + "\n"
+
+    def plan(self, staging_bytes: int) -> dict:
+        p = _PackPlan()
+        _check(_gguf_plan(self.h, staging_bytes, C.byref(p)))
+        return {f: getattr(p, f) for f, _ in _PackPlan._fields_}
+
+    def close(self, _close=_gguf_close):
+        if getattr(self, "h", None):
+            _close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+def ggml_row_bytes(ggml_type: int, n: int) -> int:
+    return _ggml_row_bytes(ggml_type, n)
+
+
+def gguf_open_raw(path: str, header_only: bool = False) -> int:
+    """Status code of btf_hip_gguf_open (the file is closed at once)."""
+    h = C.c_void_p()
+    rc = _gguf_open(os.fsencode(path), int(header_only), C.byref(h))
+    if rc == BTF_OK:
+        _gguf_close(h.value)
+    return rc
+
+
+class Loader:
+    """Staged PTQ1_0 -> T2 upload through two pinned slots (btf_hip_loader_*)."""
+
+    def __init__(self, staging_bytes: int):
+        h = C.c_void_p()
+        _check(_loader_create(staging_bytes, C.byref(h)))
+        self.h = h.value
+
+    def upload_ptq1_0(self, src, N: int, K: int, codes, scales, stream=None):
+        """src: host address / numpy array of N*K/128*28 bytes; codes/scales: device."""
+        if hasattr(src, "ctypes"):
+            src = src.ctypes.data
+        _check(_loader_upload(self.h, src, N, K, _addr(codes), _addr(scales), _stream(stream)))
+
+    def upload_raw(self, src, N, K, codes, scales, stream=None) -> int:
+        if hasattr(src, "ctypes"):
+            src = src.ctypes.data
+        return _loader_upload(self.h, src, N, K, _addr(codes), _addr(scales), _stream(stream))
+
+    def finish(self) -> int:
+        n = C.c_uint64()
+        _check(_loader_finish(self.h, C.byref(n)))
+        return n.value
+
+    def close(self, _destroy=_loader_destroy):
+        if getattr(self, "h", None):
+            _destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
+
+
+def loader_create_raw(staging_bytes: int) -> int:
+    h = C.c_void_p()
+    rc = _loader_create(staging_bytes, C.byref(h))
+    if rc == BTF_OK:
+        _loader_destroy(h.value)
+    return rc
 
 
 def lib_path() -> str:

@@ -203,6 +203,93 @@ int btf_hip_step_destroy(btf_step_t prog);
  * makes a launch give up waiting and set the error flag instead of hanging. */
 int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls);
 
+/* ---- load path: GGUF reader -> pinned double-buffered staging -> repack --
+ * The reference decoder reads its model with bd::Gguf
+ * (ref/bonsai-decoder/include/bd/gguf.hpp:49-85, src/gguf.cpp:73-147),
+ * uploads each PTQ1_0 matrix with GpuDecoder::upload_mat / upload
+ * (src/cuda/gpu_decoder.cu:284-393: slices of rows through two pinned
+ * staging slots, launch_repack on each) and sizes the resident layout with
+ * plan_memory (src/repack.cpp:142-204). These entry points provide the same
+ * three steps; a decoder keeps its own model binding on top.
+ *
+ * The reader memory-maps the file read-only and parses GGUF v2/v3 in one
+ * pass, with the reference's checks (a bad or truncated file fails with
+ * BTF_ERR_ARGS and the reason). Tensor data stay in the mapping: `data`
+ * points into it (NULL for a tensor past the end of a header-only read) and
+ * stays valid until btf_hip_gguf_close. Strings and names are owned by the
+ * reader. ne[] is ggml order: ne[0] is contiguous (for a matrix, K), unused
+ * dimensions are 1. Numeric metadata keep an integer and a double form
+ * (integers convert exactly, floats truncate to the integer form, booleans
+ * are 0 or 1); a key present twice resolves to its last entry. */
+typedef void* btf_gguf_t;
+typedef struct btf_gguf_header {
+  uint32_t version;     /* 2 or 3 */
+  uint64_t alignment;   /* general.alignment, default 32 */
+  uint64_t data_offset; /* start of the data section in the file */
+  uint64_t file_bytes;
+  int64_t n_tensors, n_kv;
+} btf_gguf_header;
+typedef struct btf_gguf_tensor {
+  const char* name;
+  int n_dims;
+  int64_t ne[4];
+  uint32_t type;   /* ggml type id (PTQ1_0 = 143, F32 = 0, F16 = 1, ...) */
+  uint64_t offset; /* in the data section */
+  uint64_t bytes;
+  const uint8_t* data;
+} btf_gguf_tensor;
+typedef struct btf_gguf_kv {
+  const char* key; /* key_len bytes (may hold NUL bytes) */
+  uint64_t key_len;
+  uint32_t type;     /* GGUF value type: 0 U8 ... 8 STRING, 9 ARRAY, 10 U64, 11 I64, 12 F64 */
+  uint32_t arr_type; /* element type of an array */
+  uint64_t len;      /* elements (1 for a scalar) */
+} btf_gguf_kv;
+int btf_hip_gguf_open(const char* path, int header_only, btf_gguf_t* out);
+int btf_hip_gguf_close(btf_gguf_t g);
+int btf_hip_gguf_info(btf_gguf_t g, btf_gguf_header* out);
+int btf_hip_gguf_tensor(btf_gguf_t g, int64_t index, btf_gguf_tensor* out);
+int64_t btf_hip_gguf_find_tensor(btf_gguf_t g, const char* name); /* -1: absent */
+int btf_hip_gguf_kv(btf_gguf_t g, int64_t index, btf_gguf_kv* out);
+int64_t btf_hip_gguf_find_kv(btf_gguf_t g, const char* key);      /* -1: absent */
+/* Element `elem` (0 for a scalar) of a numeric value / of a string value. */
+int btf_hip_gguf_kv_num(btf_gguf_t g, int64_t index, uint64_t elem, int64_t* i, double* f);
+int btf_hip_gguf_kv_str(btf_gguf_t g, int64_t index, uint64_t elem, const char** s, uint64_t* len);
+/* Bytes of n elements of a ggml type (-1: unknown type or n not whole
+ * blocks), as bd::row_bytes (ref/bonsai-decoder/src/types.cpp:36-40). */
+int64_t btf_hip_ggml_row_bytes(uint32_t type, int64_t n);
+
+/* Resident bytes of the file's PTQ1_0 matrices (2-D tensors of type 143,
+ * K = ne[0], N = ne[1]) in the T2 layout, and the staging of a load with
+ * slots of staging_bytes. arena_bytes rounds every codes and scales array
+ * up to 256 B (one allocation holding them all). */
+typedef struct btf_pack_plan {
+  int64_t n_matrices;
+  uint64_t codes_bytes, scales_bytes, arena_bytes;
+  uint64_t source_bytes; /* their PTQ1_0 bytes in the file */
+  uint64_t other_bytes;  /* every other tensor's bytes */
+  uint64_t staging_host_bytes, staging_device_bytes; /* 2 slots each, freed after the load */
+} btf_pack_plan;
+int btf_hip_gguf_plan(btf_gguf_t g, uint64_t staging_bytes, btf_pack_plan* out);
+
+/* Staged upload of PTQ1_0 rows src [N][K/128][28] (host memory: a GGUF
+ * mapping, or any buffer) into the T2 layout codes [N][K/4], scales
+ * [N][K/128] (device). Slices of whole rows go through two pinned host slots
+ * of staging_bytes in turn: the host copies a slice into a slot once the
+ * slot's previous slice is done, the copy engine moves it into a device slot
+ * and the repack kernel writes the packed rows, all on `stream`, so the host
+ * copy of one slice overlaps the device's work on the other. Uploads return
+ * once their last slice is queued (src may then be reused); finish waits for
+ * every queued slice. A loader belongs to the device current at creation
+ * (btf_hip_kernels_init must have run for it) and allocates its slots once;
+ * uploads allocate nothing. */
+typedef void* btf_loader_t;
+int btf_hip_loader_create(uint64_t staging_bytes, btf_loader_t* out);
+int btf_hip_loader_upload_ptq1_0(btf_loader_t L, const uint8_t* src, int64_t N, int64_t K, uint8_t* codes,
+                                 uint16_t* scales, btf_stream_t stream);
+int btf_hip_loader_finish(btf_loader_t L, uint64_t* source_bytes); /* total PTQ1_0 bytes uploaded */
+int btf_hip_loader_destroy(btf_loader_t L);
+
 /* Device description for reports. name must hold name_len bytes. */
 typedef struct btf_device_info {
   int cu_count;

@@ -11,6 +11,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <utility>
 
 #include "hip_abi.h"
 
@@ -134,6 +135,107 @@ class StepProgram {
 
  private:
   btf_step_t p_ = nullptr;
+};
+
+// ---- load path (no counterpart in kernels.cuh): the reader of the model file
+// and the staged upload. Gguf offers what the reference's bd::Gguf offers for
+// loading (ref/bonsai-decoder/include/bd/gguf.hpp:49-85: open, tensor lookup,
+// need_tensor, get_i / get_f / get_s / get_b); Loader is GpuDecoder::upload_mat
+// (src/cuda/gpu_decoder.cu:284-300) as an object. Both throw
+// std::runtime_error on failure.
+struct GgufTensor {
+  std::string name;
+  int n_dims = 0;
+  int64_t ne[4] = {1, 1, 1, 1};
+  uint32_t type = 0;
+  uint64_t offset = 0, bytes = 0;
+  const uint8_t* data = nullptr;
+  int64_t n_elements() const { return ne[0] * ne[1] * ne[2] * ne[3]; }
+  int64_t dim(int d) const { return d < n_dims ? ne[d] : 1; }
+};
+
+class Gguf {
+ public:
+  explicit Gguf(const std::string& path, bool header_only = false) {
+    detail::check(btf_hip_gguf_open(path.c_str(), header_only ? 1 : 0, &g_), "gguf_open");
+    detail::check(btf_hip_gguf_info(g_, &h_), "gguf_info");
+  }
+  Gguf(const Gguf&) = delete;
+  Gguf& operator=(const Gguf&) = delete;
+  ~Gguf() { (void)btf_hip_gguf_close(g_); }
+  uint32_t version() const { return h_.version; }
+  uint64_t alignment() const { return h_.alignment; }
+  uint64_t data_offset() const { return h_.data_offset; }
+  int64_t n_tensors() const { return h_.n_tensors; }
+  GgufTensor tensor_at(int64_t i) const {
+    btf_gguf_tensor t;
+    detail::check(btf_hip_gguf_tensor(g_, i, &t), "gguf_tensor");
+    GgufTensor r;
+    r.name = t.name;
+    r.n_dims = t.n_dims;
+    for (int d = 0; d < 4; ++d) r.ne[d] = t.ne[d];
+    r.type = t.type;
+    r.offset = t.offset;
+    r.bytes = t.bytes;
+    r.data = t.data;
+    return r;
+  }
+  bool has_tensor(const std::string& name) const { return btf_hip_gguf_find_tensor(g_, name.c_str()) >= 0; }
+  GgufTensor need_tensor(const std::string& name) const {
+    const int64_t i = btf_hip_gguf_find_tensor(g_, name.c_str());
+    if (i < 0) throw std::runtime_error("missing tensor " + name);
+    return tensor_at(i);
+  }
+  bool has(const std::string& key) const { return btf_hip_gguf_find_kv(g_, key.c_str()) >= 0; }
+  int64_t get_i(const std::string& key) const { return num(key).first; }
+  int64_t get_i(const std::string& key, int64_t def) const { return has(key) ? get_i(key) : def; }
+  double get_f(const std::string& key) const { return num(key).second; }
+  double get_f(const std::string& key, double def) const { return has(key) ? get_f(key) : def; }
+  bool get_b(const std::string& key, bool def) const { return has(key) ? get_i(key) != 0 : def; }
+  std::string get_s(const std::string& key, const std::string& def = "") const {
+    const int64_t i = btf_hip_gguf_find_kv(g_, key.c_str());
+    const char* s = nullptr;
+    uint64_t n = 0;
+    if (i < 0 || btf_hip_gguf_kv_str(g_, i, 0, &s, &n) != BTF_OK) return def;
+    return std::string(s, (size_t)n);
+  }
+  btf_pack_plan plan(uint64_t staging_bytes) const {
+    btf_pack_plan p;
+    detail::check(btf_hip_gguf_plan(g_, staging_bytes, &p), "gguf_plan");
+    return p;
+  }
+  btf_gguf_t handle() const { return g_; }
+
+ private:
+  std::pair<int64_t, double> num(const std::string& key) const {
+    const int64_t i = btf_hip_gguf_find_kv(g_, key.c_str());
+    if (i < 0) throw std::runtime_error("gguf: missing key " + key);
+    int64_t v = 0;
+    double f = 0.0;
+    detail::check(btf_hip_gguf_kv_num(g_, i, 0, &v, &f), "gguf_kv_num");
+    return {v, f};
+  }
+  btf_gguf_t g_ = nullptr;
+  btf_gguf_header h_{};
+};
+
+class Loader {
+ public:
+  explicit Loader(uint64_t staging_bytes) { detail::check(btf_hip_loader_create(staging_bytes, &l_), "loader_create"); }
+  Loader(const Loader&) = delete;
+  Loader& operator=(const Loader&) = delete;
+  ~Loader() { (void)btf_hip_loader_destroy(l_); }
+  void upload_ptq1_0(const uint8_t* src, int64_t N, int64_t K, uint8_t* codes, uint16_t* scales, btf_stream_t st) {
+    detail::check(btf_hip_loader_upload_ptq1_0(l_, src, N, K, codes, scales, st), "loader_upload");
+  }
+  uint64_t finish() {
+    uint64_t n = 0;
+    detail::check(btf_hip_loader_finish(l_, &n), "loader_finish");
+    return n;
+  }
+
+ private:
+  btf_loader_t l_ = nullptr;
 };
 
 }  // namespace hip

@@ -246,6 +246,21 @@ class Ref:
               [_p, _i32, _i32, _p, C.c_float, _i32, _i32, _i32, _i32, _p, _p, _p, _p, _p])
         _decl(L, "ref_emu_embed", _i32, [_p, _p, _p, _i32, _i32, _i32, _i32, _p, _p])
         _decl(L, "ref_argmax", _i32, [_p, _i32])
+        _decl(L, "ref_gguf_dump", _i32, [C.c_char_p, _i32, C.c_char_p, C.c_size_t])
+        _decl(L, "ref_gguf_write_example", _i32, [C.c_char_p, C.c_uint32, C.c_uint64])
+
+    def gguf_dump(self, path, header_only=False):
+        """(ok, text): the reference reader's canonical dump of a GGUF file,
+        or its error message."""
+        buf = C.create_string_buffer(1 << 22)
+        rc = self.lib.ref_gguf_dump(os.fsencode(path), int(header_only), buf, len(buf))
+        if rc == -2:
+            raise RuntimeError("ref_gguf_dump: output buffer too small")
+        return rc == 0, buf.value.decode()
+
+    def gguf_write_example(self, path, alignment=32, seed=1):
+        if self.lib.ref_gguf_write_example(os.fsencode(path), alignment, seed) != 0:
+            raise RuntimeError("ref_gguf_write_example failed")
 
     def quant_ptq1_0(self, w):
         w = np.ascontiguousarray(w, np.float32)

@@ -225,4 +225,102 @@ int ref_emu_prep(const float* x, int M, int n, const float* normw, float eps, in
   }
 }
 
+// ---- GGUF (ref/bonsai-decoder/src/gguf.cpp) ----
+// Canonical text of everything bd::Gguf parsed from `path` (one line per
+// header field, metadata key and tensor; strings in hex), written into out.
+// Returns 0, or -1 with the reader's error message in out.
+int ref_gguf_dump(const char* path, int header_only, char* out, size_t cap) {
+  std::string txt;
+  try {
+    std::unique_ptr<bd::Gguf> g = bd::Gguf::open(path, header_only != 0);
+    std::ostringstream o;
+    auto hex = [](const std::string& s) {
+      static const char* d = "0123456789abcdef";
+      std::string h;
+      for (unsigned char c : s) h += d[c >> 4], h += d[c & 15];
+      return std::to_string(s.size()) + ":" + h;
+    };
+    auto num = [](double f) {
+      char b[64];
+      std::snprintf(b, sizeof b, "%.17g", f);
+      return std::string(b);
+    };
+    o << "version " << g->version << "\nalignment " << g->alignment << "\ndata_offset " << g->data_offset
+      << "\nn_tensors " << g->tensors.size() << "\nn_kv " << g->kv_order.size() << "\n";
+    for (const std::string& k : g->kv_order) {
+      const bd::GgufValue& v = g->kv.at(k);
+      o << "kv " << hex(k) << " " << v.type;
+      if (v.type == bd::GV_ARRAY) {
+        o << " " << v.arr_type << " " << v.arr_len();
+        for (size_t j = 0; j < v.arr_len(); ++j) {
+          if (v.arr_type == bd::GV_STRING) o << " " << hex(v.as[j]);
+          else if (v.arr_type == bd::GV_F32 || v.arr_type == bd::GV_F64) o << " " << num(v.af[j]);
+          else o << " " << v.ai[j];
+        }
+      } else if (v.type == bd::GV_STRING) {
+        o << " " << hex(v.s);
+      } else {
+        o << " " << v.i << " " << num(v.f);
+      }
+      o << "\n";
+    }
+    for (const bd::GgufTensor& t : g->tensors) {
+      o << "tensor " << hex(t.name) << " " << t.type << " " << t.ne.size();
+      for (int64_t x : t.ne) o << " " << x;
+      o << " " << t.offset << " " << t.bytes << " " << (t.data ? 1 : 0) << "\n";
+    }
+    txt = o.str();
+  } catch (const std::exception& e) {
+    std::snprintf(out, cap, "%s", e.what());
+    return -1;
+  }
+  if (txt.size() + 1 > cap) return -2;
+  std::memcpy(out, txt.c_str(), txt.size() + 1);
+  return 0;
+}
+
+// A GGUF file written by the reference's own bd::GgufWriter: metadata of
+// every scalar kind and arrays, and tensors of several ggml types (PTQ1_0
+// data from a seeded byte stream), at the given alignment.
+int ref_gguf_write_example(const char* path, uint32_t alignment, uint64_t seed) {
+  try {
+    bd::GgufWriter w;
+    w.kv_str("general.architecture", "qwen35");
+    w.kv_u32("qwen35.block_count", 2);
+    w.kv_i32("test.negative", -7);
+    w.kv_f32("test.eps", 1e-6f);
+    w.kv_bool("test.flag", true);
+    w.kv_arr_i32("test.ints", {1, -2, 3, 400000});
+    w.kv_arr_f32("test.floats", {0.5f, -1.25f, 3.0e-8f});
+    w.kv_arr_str("test.strings", {"a", "", "bonsai ternary", "line\nbreak"});
+    uint64_t x = seed;
+    auto next = [&]() {
+      x += 0x9e3779b97f4a7c15ull;
+      uint64_t z = x;
+      z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+      z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+      return z ^ (z >> 31);
+    };
+    auto bytes = [&](size_t n) {
+      std::vector<uint8_t> b(n);
+      for (auto& c : b) c = (uint8_t)next();
+      return b;
+    };
+    w.tensor("blk.0.ffn_gate.weight", {256, 96}, bd::T_PTQ1_0, bytes(96 * 2 * 28));
+    w.tensor("blk.0.attn_norm.weight", {256}, bd::T_F32, bytes(256 * 4));
+    w.tensor("blk.1.ffn_down.weight", {384, 40}, bd::T_PTQ1_0, bytes(40 * 3 * 28));
+    w.tensor("blk.1.scale.weight", {64, 2}, bd::T_F16, bytes(64 * 2 * 2));
+    w.tensor("output.weight", {1024, 33}, bd::T_PTQ1_0, bytes(33 * 8 * 28));
+    const std::vector<uint8_t> img = w.finish(alignment);
+    FILE* f = std::fopen(path, "wb");
+    if (!f) return -1;
+    const size_t n = std::fwrite(img.data(), 1, img.size(), f);
+    std::fclose(f);
+    return n == img.size() ? 0 : -1;
+  } catch (const std::exception& e) {
+    std::fprintf(stderr, "ref_gguf_write_example: %s\n", e.what());
+    return -1;
+  }
+}
+
 }  // extern "C"
