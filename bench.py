@@ -386,12 +386,181 @@ def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
                       f"{total_t:.2f} s of CPU time; host CPU: {cpu_model}"}
 
 
+def write_synth_gguf(path, layers, seed=0, chunk=1 << 26):
+    """A GGUF v3 file of the 27B shapes' PTQ1_0 matrices (per layer QKV, o,
+    gate, up, down; the output projection), seeded random bytes (the PTQ1_0
+    codec decodes every byte value), plus one F32 norm per layer; streamed to
+    disk. Returns the PTQ1_0 bytes written."""
+    import struct
+    import numpy as np
+    rng = np.random.default_rng(seed)
+    mats = []
+    for l in range(layers):
+        mats += [(f"blk.{l}.attn_qkv.weight", E, QKV), (f"blk.{l}.attn_output.weight", E, E),
+                 (f"blk.{l}.ffn_gate.weight", E, F), (f"blk.{l}.ffn_up.weight", E, F),
+                 (f"blk.{l}.ffn_down.weight", F, E)]
+    mats.append(("output.weight", E, V))
+    tens = []  # (name, ne, type, bytes)
+    for l in range(layers):
+        tens.append((f"blk.{l}.attn_norm.weight", (E,), 0, 4 * E))
+    for name, K, N in mats:
+        tens.append((name, (K, N), 143, N * K // 128 * 28))
+    align = 32
+
+    def st(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    head = b"GGUF" + struct.pack("<IQQ", 3, len(tens), 2)
+    head += st("general.architecture") + struct.pack("<I", 8) + st("qwen35")
+    head += st("general.alignment") + struct.pack("<II", 4, align)
+    off, offs = 0, []
+    for name, ne, ty, nb in tens:
+        offs.append(off)
+        head += st(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", x) for x in ne)
+        head += struct.pack("<IQ", ty, off)
+        off = (off + nb + align - 1) // align * align
+    head += b"\0" * ((-len(head)) % align)
+    src = 0
+    with open(path, "wb") as f:
+        f.write(head)
+        pos = 0
+        for (name, ne, ty, nb), o in zip(tens, offs):
+            if o > pos:
+                f.write(b"\0" * (o - pos))
+            left = nb
+            while left:
+                n = min(chunk, left)
+                f.write(rng.integers(0, 256, size=n, dtype=np.uint8).tobytes())
+                left -= n
+            pos = o + nb
+            src += nb if ty == 143 else 0
+        f.write(b"\0" * (off - pos))
+    return src
+
+
+def run_load(args, hip, torch):
+    """--workload load: GGUF file -> staged upload -> resident T2 layout of
+    every PTQ1_0 matrix (btf_hip_gguf_* + btf_hip_loader_*), from the page
+    cache; `value` = PTQ1_0 bytes read from the file / wall time of the whole
+    upload (open, plan, every upload, finish), median of the timed loads."""
+    import tempfile
+    import numpy as np
+    staging = 64 << 20
+    tmp = tempfile.mkdtemp(prefix="btf_load_")
+    path = os.path.join(tmp, "synth.gguf")
+    layers = args.layers if args.layers != LAYERS else 8
+    t0 = time.time()
+    src_bytes = write_synth_gguf(path, layers)
+    log(f"synthetic GGUF: {layers} layers + output, {os.path.getsize(path) / 1e9:.3f} GB file "
+        f"({src_bytes / 1e9:.3f} GB of PTQ1_0) written in {time.time() - t0:.1f} s")
+    with open(path, "rb") as f:  # into the page cache
+        while f.read(1 << 26):
+            pass
+    arena, times, plan = None, [], None
+    for rep in range(args.warmup + args.steps):
+        t0 = time.perf_counter()
+        g = hip.Gguf(path)
+        plan = g.plan(staging)
+        if arena is None:
+            arena = torch.empty(plan["arena_bytes"], dtype=torch.uint8, device="cuda")
+        L = hip.Loader(staging)
+        st = torch.cuda.current_stream().cuda_stream
+        off, base = 0, arena.data_ptr()
+        for t in g.tensors:
+            if t.type != 143 or t.n_dims != 2:
+                continue
+            K, N = t.ne
+            co = off
+            so = co + (N * K // 4 + 255) // 256 * 256
+            off = so + (N * K // 64 + 255) // 256 * 256
+            L.upload_ptq1_0(t.data, N, K, base + co, base + so, st)
+        n = L.finish()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        L.close()
+        g.close()
+        assert n == plan["source_bytes"] == src_bytes
+        if rep >= args.warmup:
+            times.append(dt)
+    t = float(np.median(times))
+    value = src_bytes / t / 1e9
+    log(f"load: {t * 1e3:.1f} ms for {src_bytes / 1e9:.3f} GB of PTQ1_0 -> {plan['arena_bytes'] / 1e9:.3f} GB "
+        f"resident: {value:.2f} GB/s")
+    # stage rates on one 64 MiB slice: host copy from the mapping, DMA copy, repack kernel
+    g = hip.Gguf(path)
+    tm = g.tensor("blk.0.ffn_gate.weight")
+    rows = staging // (tm.ne[0] // 128 * 28)
+    nbytes = rows * (tm.ne[0] // 128 * 28)
+    import ctypes as C
+    pinned = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        C.memmove(pinned.data_ptr(), tm.data, nbytes)
+    host_gbs = 5 * nbytes / (time.perf_counter() - t0) / 1e9
+    dstage = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    e0, e1 = hip.Event(), hip.Event()
+    st = torch.cuda.current_stream().cuda_stream
+    e0.record(st)
+    for _ in range(5):
+        dstage.copy_(pinned, non_blocking=True)
+    e1.record(st)
+    torch.cuda.synchronize()
+    dma_gbs = 5 * nbytes / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    codes = torch.empty(rows * tm.ne[0] // 4, dtype=torch.uint8, device="cuda")
+    scales = torch.empty(rows * tm.ne[0] // 128, dtype=torch.int16, device="cuda")
+    e0.record(st)
+    for _ in range(5):
+        hip.launch_repack(dstage, rows * tm.ne[0] // 128, codes, scales, st)
+    e1.record(st)
+    torch.cuda.synchronize()
+    rep_gbs = 5 * nbytes / (e0.elapsed_ms(e1) * 1e-3) / 1e9
+    log(f"stages on a {nbytes / 2**20:.0f} MiB slice: host copy from the mapping {host_gbs:.2f} GB/s, "
+        f"copy engine {dma_gbs:.2f} GB/s, repack kernel {rep_gbs:.1f} GB/s (of PTQ1_0 read)")
+    g.close()
+    cpu = None
+    if not args.no_cpu:
+        sys.path.insert(0, ORACLE)
+        from btf_oracle import Oracle, Ref, have_ref
+        kind = "reference" if have_ref() else "port"
+        R = Ref() if kind == "reference" else Oracle()
+        g = hip.Gguf(path)
+        tm = g.tensor("blk.0.ffn_down.weight")
+        K, N = tm.ne
+        srcm = np.frombuffer(C.string_at(tm.data, tm.bytes), dtype=np.uint8).reshape(N, K // 128 * 28)
+        done, tt = 0, 0.0
+        while tt < min(args.cpu_budget, 6.0):
+            t0 = time.perf_counter()
+            R.repack_rows(srcm, N, K)
+            tt += time.perf_counter() - t0
+            done += srcm.size
+        g.close()
+        cpu = {"value": round(done / tt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+               "sample": f"host repack of the 5120 x 17408 down matrix ({srcm.size / 1e6:.1f} MB of PTQ1_0), "
+                         f"{done // srcm.size} passes, {tt:.2f} s; "
+                         f"{'reference btf::repack_rows (src/repack.cpp:16-27) built from the reference sources' if kind == 'reference' else 'oracle port of repack_rows'}, one thread"}
+    os.remove(path)
+    os.rmdir(tmp)
+    out = {
+        "metric": "PTQ1_0 GGUF load GB/s (file in page cache -> resident T2 layout)", "value": round(value, 2),
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic GGUF (seeded PTQ1_0 bytes) of the 27B shapes",
+        "config": {"workload": f"load {layers} layers x (QKV, o, gate, up, down) + output projection, "
+                               f"{src_bytes} B of PTQ1_0 -> {plan['arena_bytes']} B resident, 2 x 64 MiB staging",
+                   "parallelism": "single GPU"},
+        "stages_gbs": {"host_copy": round(host_gbs, 2), "copy_engine": round(dma_gbs, 2),
+                       "repack_kernel": round(rep_gbs, 1)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill"])
+    ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill", "load"])
     ap.add_argument("--batch", type=int, default=0, help="M for --workload batched (default 4,8,16,32 sweep)")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -427,6 +596,10 @@ def main():
         torch.cuda.synchronize()
         log("calibration: 3 device copies of 1 GiB (reads 1 GiB, writes 1 GiB each)")
         del a, b
+
+    if args.workload == "load":
+        run_load(args, hip, torch)
+        return
 
     layers = args.layers if args.workload == "sweep" else (1 if args.workload == "layer" else 8)
     t0 = time.time()

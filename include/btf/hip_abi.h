@@ -275,8 +275,9 @@ int btf_hip_gguf_plan(btf_gguf_t g, uint64_t staging_bytes, btf_pack_plan* out);
 /* Staged upload of PTQ1_0 rows src [N][K/128][28] (host memory: a GGUF
  * mapping, or any buffer) into the T2 layout codes [N][K/4], scales
  * [N][K/128] (device). Slices of whole rows go through two pinned host slots
- * of staging_bytes in turn: the host copies a slice into a slot once the
- * slot's previous slice is done, the copy engine moves it into a device slot
+ * of staging_bytes in turn: the host copies a slice into a slot (on up to 8
+ * threads) once the slot's previous slice is done, the copy engine moves it
+ * into a device slot
  * and the repack kernel writes the packed rows, all on `stream`, so the host
  * copy of one slice overlaps the device's work on the other. Uploads return
  * once their last slice is queued (src may then be reused); finish waits for

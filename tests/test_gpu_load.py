@@ -30,7 +30,10 @@ def oracle_repack(oracle, src, N, K):
 def test_loader_slices_byte_exact(hip, oracle):
     torch = _torch()
     rng = np.random.default_rng(41)
-    for N, K, staging in [(37, 1024, 3 * 8 * 28 + 5), (64, 5120, 40 * 28), (5, 128, 28), (300, 2048, 1 << 20)]:
+    # small slots (many slices, both slots, a short last slice, one row per
+    # slice) and large ones (the host copy of a slice split over threads)
+    for N, K, staging in [(37, 1024, 3 * 8 * 28 + 5), (64, 5120, 40 * 28), (5, 128, 28), (300, 2048, 1 << 20),
+                          (8192, 5120, 16 << 20), (20000, 5120, 12 << 20)]:
         src = gw.ptq1_0_bytes(rng, N, K)
         codes = torch.full((N * K // 4,), 0xEE, dtype=torch.uint8, device="cuda")
         scales = torch.full((N * K // 128,), -1, dtype=torch.int16, device="cuda")
