@@ -75,6 +75,11 @@ def gemv_bytes(N, K, M, out_rw=1, nmat=1):
     return nmat * (N * K // 4 + N * K // 64) + M * (K + K // 4) + 4 * M * N * out_rw
 
 
+def b3_bytes(N, K, M, out_rw=1, nmat=1):
+    """The same GEMV reading PTQ1_0 blocks directly: 28 B per 128 weights."""
+    return nmat * (N * K // 128 * 28) + M * (K + K // 4) + 4 * M * N * out_rw
+
+
 def prep_bytes(K, M):
     return M * (4 * K + K + K // 4)
 
@@ -82,7 +87,9 @@ def prep_bytes(K, M):
 class Setup:
     """Weights of every matrix of the sweep, resident in one device arena."""
 
-    def __init__(self, hip, torch, layers, seed=0):
+    def __init__(self, hip, torch, layers, seed=0, keep_src=False):
+        """keep_src: also keep every matrix's PTQ1_0 rows resident (for the
+        GEMV that reads them directly)."""
         self.hip, self.torch = hip, torch
         shapes = []  # (name, layer, N, K, matrix id)
         for l in range(layers):
@@ -99,14 +106,20 @@ class Setup:
         self.arena_bytes = off
         self.arena = torch.empty(off, dtype=torch.uint8, device="cuda")
         base = self.arena.data_ptr()
+        self.src_off, soff = {}, 0
+        for key, (N, K, _, _, _) in self.mats.items():
+            self.src_off[key] = soff
+            soff = align(soff + N * K // 128 * 28)
+        self.src = torch.empty(soff if keep_src else 0, dtype=torch.uint8, device="cuda")
         maxblk = max(N * K // 128 for N, K, _, _, _ in self.mats.values())
-        stage = torch.empty(maxblk * 28, dtype=torch.uint8, device="cuda")
+        stage = torch.empty(0 if keep_src else maxblk * 28, dtype=torch.uint8, device="cuda")
         st = torch.cuda.current_stream().cuda_stream
         t0 = time.time()
         for (name, l), (N, K, mid, co, so) in self.mats.items():
             nb = N * K // 128
-            hip.gen_ptq1_0(seed, mid, 0, nb, stage, st)
-            hip.launch_repack(stage, nb, base + co, base + so, st)
+            src = self.src.data_ptr() + self.src_off[(name, l)] if keep_src else stage.data_ptr()
+            hip.gen_ptq1_0(seed, mid, 0, nb, src, st)
+            hip.launch_repack(src, nb, base + co, base + so, st)
         torch.cuda.synchronize()
         self.setup_s = time.time() - t0
         self.weight_bytes = sum(N * K // 4 + N * K // 64 for N, K, _, _, _ in self.mats.values())
@@ -116,6 +129,11 @@ class Setup:
         N, K, mid, co, so = self.mats[(name, l)]
         base = self.arena.data_ptr()
         return self.hip.GemvSeg(base + co, base + so, N, y, ldy)
+
+    def src_seg(self, name, l, y, ldy):
+        """The matrix as PTQ1_0 rows (Setup(keep_src=True))."""
+        N, K, mid, co, so = self.mats[(name, l)]
+        return self.hip.GemvSeg(self.src.data_ptr() + self.src_off[(name, l)], None, N, y, ldy)
 
     def host_mat(self, name, l):
         """(codes, scales) numpy copies of one matrix."""
@@ -151,6 +169,12 @@ class Step:
         b_gemv = {"qkv": gemv_bytes(QKV, E, M), "o": gemv_bytes(E, E, M), "gateup": gemv_bytes(F, E, M, 1, 2),
                   "down": gemv_bytes(E, F, M, 2), "output": gemv_bytes(V, E, 1)}
         self.kind_bytes = b_gemv
+        b_b3 = {"qkv": b3_bytes(QKV, E, M), "o": b3_bytes(E, E, M), "gateup": b3_bytes(F, E, M, 1, 2),
+                "down": b3_bytes(E, F, M, 2), "output": b3_bytes(V, E, 1)}
+        self.kind_bytes_b3 = b_b3
+        self.b3_total_bytes = layers * (b_b3["qkv"] + b_b3["o"] + b_b3["gateup"] + b_b3["down"]) + \
+            (b_b3["output"] + prep_bytes(E, 1) if with_output else 0) + \
+            layers * (3 * prep_bytes(E, M) + prep_bytes(F, M))
         self.gemv_bytes = layers * (b_gemv["qkv"] + b_gemv["o"] + b_gemv["gateup"] + b_gemv["down"])
         self.prep_bytes = layers * (3 * prep_bytes(E, M) + prep_bytes(F, M))
         if with_output:
@@ -205,6 +229,37 @@ class Step:
         if self.with_output:
             self.prep(self.res, E, 1, st)
             self.gemv([self.S.seg("output", self.layers, self.logits, V)], E, 1, self.S.hip.GemvMode.kStore, st)
+
+    def layer_b3(self, l, st):
+        """The layer of `layer` on the PTQ1_0 rows, read directly."""
+        S, M, G, hip = self.S, self.M, self.S.hip.GemvMode, self.S.hip
+        self.prep(self.res, E, M, st)
+        hip.launch_gemv_ptq1_0([S.src_seg("qkv", l, self.qkv, QKV)], E, M, self.act, G.kStore, st)
+        self.prep(self.xo, E, M, st)
+        hip.launch_gemv_ptq1_0([S.src_seg("o", l, self.x, E)], E, M, self.act, G.kStore, st)
+        self.prep(self.x, E, M, st)
+        hip.launch_gemv_ptq1_0([S.src_seg("gate", l, self.h, F), S.src_seg("up", l, None, 0)], E, M, self.act,
+                               G.kSwiglu, st)
+        self.prep(self.h, F, M, st)
+        hip.launch_gemv_ptq1_0([S.src_seg("down", l, self.res, E)], F, M, self.act, G.kAdd, st)
+
+    def run_b3(self, st):
+        for l in range(self.layers):
+            self.layer_b3(l, st)
+        if self.with_output:
+            self.prep(self.res, E, 1, st)
+            self.S.hip.launch_gemv_ptq1_0([self.S.src_seg("output", self.layers, self.logits, V)], E, 1, self.act,
+                                          self.S.hip.GemvMode.kStore, st)
+
+    def kind_launch_b3(self, kind, l, st):
+        S, M, G, hip = self.S, self.M, self.S.hip.GemvMode, self.S.hip
+        segs, K, mode = {
+            "qkv": ([S.src_seg("qkv", l, self.qkv, QKV)], E, G.kStore),
+            "o": ([S.src_seg("o", l, self.x, E)], E, G.kStore),
+            "gateup": ([S.src_seg("gate", l, self.h, F), S.src_seg("up", l, None, 0)], E, G.kSwiglu),
+            "down": ([S.src_seg("down", l, self.res, E)], F, G.kAdd),
+            "output": ([S.src_seg("output", self.layers, self.logits, V)], E, G.kStore)}[kind]
+        hip.launch_gemv_ptq1_0(segs, K, 1 if kind == "output" else M, self.act, mode, st)
 
     def reset(self):
         self.res.copy_(self.S.torch.from_numpy(self.res0).cuda())
@@ -569,6 +624,9 @@ def main():
                     help="auto: at batch 1 every engine is timed and the fastest one is the value; "
                          "the graph otherwise")
     ap.add_argument("--no-kinds", action="store_true", help="skip the per-GEMV-kind graph timings")
+    ap.add_argument("--b3", dest="b3", action="store_true", default=None,
+                    help="also time the chain on the PTQ1_0 rows read directly (default: with --engine auto)")
+    ap.add_argument("--no-b3", dest="b3", action="store_false")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run 3 device copies of 1 GiB (the scale reference for HBM counters)")
     args = ap.parse_args()
@@ -603,7 +661,8 @@ def main():
 
     layers = args.layers if args.workload == "sweep" else (1 if args.workload == "layer" else 8)
     t0 = time.time()
-    S = Setup(hip, torch, layers)
+    with_b3 = (args.engine == "auto" if args.b3 is None else args.b3) and args.workload in ("sweep", "layer")
+    S = Setup(hip, torch, layers, keep_src=with_b3)
     log(f"weights generated + repacked: {S.arena_bytes / 1e9:.3f} GB arena in {time.time() - t0:.2f} s")
 
     if args.workload == "sweep":
@@ -648,6 +707,30 @@ def main():
         step.reset()
         engine_ms["graph"], g = time_graph(hip, torch, step.run, args.steps, args.warmup)
         log(f"graph engine: {engine_ms['graph']:.4f} ms per step")
+    # The same chain on the PTQ1_0 rows read directly (btf_hip_launch_gemv_ptq1_0
+    # in a graph of quantize + GEMV launches): checked bit-exact against the
+    # graph engine, rated on its own algorithmic bytes (28 B per 128 weights).
+    b3 = None
+    if with_b3:
+        ok, why = verify_vs_graph(torch, step, lambda st: step.run_b3(st))
+        log(f"PTQ1_0-direct launches vs op-by-op launches: {why}")
+        if not ok:
+            raise SystemExit(f"PTQ1_0-direct launches do not match the op-by-op launches: {why}")
+        step.reset()
+        b3_ms, _ = time_graph(hip, torch, step.run_b3, args.steps, args.warmup)
+        b3 = {"ms_per_step": round(b3_ms, 4), "bytes_per_step": step.b3_total_bytes,
+              "GBs": round(step.b3_total_bytes / (b3_ms / 1e3) / 1e9, 1), "tok_s_equiv": round(1e3 / b3_ms, 2),
+              "verified": why, "kinds": {}}
+        log(f"PTQ1_0-direct graph: {b3_ms:.4f} ms per step, {b3['GBs']} GB/s of its own bytes")
+        for kind in ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else []):
+            reps = 1 if kind == "output" else layers
+            fn = (lambda st, kind=kind: step.kind_launch_b3(kind, 0, st)) if kind == "output" else \
+                 (lambda st, kind=kind: [step.kind_launch_b3(kind, l, st) for l in range(layers)])
+            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            avg_us = kms * 1e3 / reps
+            bb = step.kind_bytes_b3[kind]
+            b3["kinds"][kind] = {"avg_us": round(avg_us, 3), "bytes": bb, "GBs": round(bb / (avg_us * 1e-6) / 1e9, 1)}
+            log(f"  PTQ1_0-direct {kind}: {avg_us:.3f} us/launch, {b3['kinds'][kind]['GBs']} GB/s")
     engine = min(engine_ms, key=engine_ms.get)
     ms = engine_ms[engine]
     kernels_per_step = {"step": 1, "chain": layers * 5 + (2 if step.with_output else 0)}.get(
@@ -771,6 +854,7 @@ def main():
         "engines_ms": {k: round(v, 4) for k, v in engine_ms.items()},
         "gemv_kinds": per,
         "decode_step_ends": ends,
+        "ptq1_0_direct": b3,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},
     }
     if not args.no_cpu:

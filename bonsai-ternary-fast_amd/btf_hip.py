@@ -101,6 +101,8 @@ _launch_argmax = _decl("btf_hip_launch_argmax", [_vp, _i, _vp, _vp, _vp])
 _launch_pos_add = _decl("btf_hip_launch_pos_add", [_vp, _i, _vp])
 _launch_gemv_ex = _decl("btf_hip_launch_gemv_ex", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _vp, _i, _i,
                                                     C.POINTER(_Q8Act), _vp])
+_launch_gemv_ptq1_0 = _decl("btf_hip_launch_gemv_ptq1_0",
+                            [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _i, _vp])
 _dump = _decl("btf_hip_gemv_i32_dump", [_vp, _i, _i, _i, C.POINTER(_Q8Act), _vp, _vp])
 _set_policy = _decl("btf_hip_gemv_set_policy", [_i])
 _gen = _decl("btf_hip_gen_ptq1_0", [C.c_uint64, C.c_uint64, _i64, _i64, _vp, _vp])
@@ -141,7 +143,7 @@ _loader_destroy = _decl("btf_hip_loader_destroy", [_vp])
 #: Every symbol include/btf/hip_abi.h declares (checked by the CPU tests).
 ABI_SYMBOLS = (
     "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
-    "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_launch_embed", "btf_hip_argmax_part_bytes",
+    "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_launch_gemv_ptq1_0", "btf_hip_launch_embed", "btf_hip_argmax_part_bytes",
     "btf_hip_launch_argmax", "btf_hip_launch_pos_add", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
     "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
     "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
@@ -296,6 +298,18 @@ def launch_gemv_ex_raw(segs, nseg: int, K: int, M: int, a, x, ldx: int, mode: in
     qa = C.byref(a._c()) if a is not None else None
     qo = C.byref(out._c()) if out is not None else None
     return _launch_gemv_ex(arr, nseg, K, M, qa, _addr(x), ldx, mode, qo, _stream(stream))
+
+
+def launch_gemv_ptq1_0(segs, K: int, M: int, a: Q8Act, mode: GemvMode = GemvMode.kStore, stream=None) -> None:
+    """launch_gemv on PTQ1_0 matrices read directly: each GemvSeg's codes are
+    N rows of K/128 28-byte PTQ1_0 blocks and its scales None."""
+    _check(launch_gemv_ptq1_0_raw(segs, len(segs), K, M, a, int(mode), stream))
+
+
+def launch_gemv_ptq1_0_raw(segs, nseg: int, K: int, M: int, a: Q8Act, mode: int, stream=None) -> int:
+    arr = (_GemvSeg * max(1, len(segs)))(*[s._c() for s in segs]) if segs else None
+    q = a._c()
+    return _launch_gemv_ptq1_0(arr, nseg, K, M, C.byref(q), mode, _stream(stream))
 
 
 def launch_gemv_raw(segs, nseg: int, K: int, M: int, a: Q8Act, mode: int, stream=None) -> int:

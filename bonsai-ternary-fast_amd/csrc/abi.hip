@@ -249,6 +249,36 @@ int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, con
   return BTF_OK;
 }
 
+int btf_hip_launch_gemv_ptq1_0(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, int mode,
+                               btf_stream_t stream) {
+  if (M <= 0) return BTF_OK;
+  if (!segs) return fail(BTF_ERR_ARGS, "gemv_ptq1_0: null segments");
+  if (K > 32768) return fail(BTF_ERR_ARGS, "gemv_ptq1_0: K > 32768");
+  // the checks of launch_gemv, with the blocks' own scales (a placeholder passes the scale check)
+  // (16-byte placeholders pass the T2 alignment checks; the blocks need 4 bytes)
+  btf_gemv_seg sv[3];
+  for (int i = 0; i < nseg && i < 3; ++i) {
+    sv[i] = segs[i];
+    if (segs[i].N == 0) continue;
+    if (segs[i].scales) return fail(BTF_ERR_ARGS, "gemv_ptq1_0: scales must be NULL (they are inside the blocks)");
+    if (!aligned(segs[i].codes, 4)) return fail(BTF_ERR_ARGS, "gemv_ptq1_0: blocks must be 4-byte aligned");
+    sv[i].codes = segs[i].codes ? reinterpret_cast<const uint8_t*>(16) : nullptr;
+    sv[i].scales = reinterpret_cast<const uint16_t*>(16);
+  }
+  int rc = check_gemv(sv, nseg, K, M, a, mode, true);
+  if (rc != BTF_OK) return rc;
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  GemvSeg sg[3];
+  for (int i = 0; i < nseg; ++i) sg[i] = {segs[i].codes, nullptr, segs[i].N, segs[i].y, segs[i].ldy};
+  const Q8 q{a->q, a->d, a->s};
+  for (int m0 = 0; m0 < M; m0 += 2) {
+    rc = gemv_b3(sg, nseg, K, m0, M - m0 < 2 ? M - m0 : 2, q, mode, static_cast<hipStream_t>(stream), *ds);
+    if (rc != BTF_OK) return rc;
+  }
+  return BTF_OK;
+}
+
 int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q8act* a, int32_t* I_out,
                           btf_stream_t stream) {
   if (M <= 0 || N <= 0) return BTF_OK;

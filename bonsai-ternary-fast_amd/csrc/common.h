@@ -159,6 +159,9 @@ int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a,
               hipStream_t st, const DevState& ds, const float* x = nullptr, int ldx = 0,
               const Q8* qout = nullptr);
 // int8 MFMA path: rows m0 .. m0+nb-1.
+// PTQ1_0 path (codes = PTQ1_0 rows, scales unused): rows m0 .. m0+nb-1 (nb <= 2), K <= 32768.
+int gemv_b3(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a, int mode, hipStream_t st,
+            const DevState& ds);
 int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a, int mode, int32_t* dump,
               hipStream_t st, const DevState& ds);
 int mfma_rows_per_pass();

@@ -149,6 +149,17 @@ int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q
 int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, const float* x,
                            int ldx, int mode, const btf_q8act* out, btf_stream_t stream);
 
+/* launch_gemv on PTQ1_0 matrices read directly (1.75 bits per weight, no T2
+ * repack): segs[i].codes points at N rows of K/128 PTQ1_0 blocks (28 bytes
+ * each: 26 bytes of base-3 digits, fp16 scale; 4-byte aligned) and
+ * segs[i].scales must be NULL. Modes, segments, y/ldy and the Q8 activation
+ * as in launch_gemv; K <= 32768. The outputs are bit-identical to
+ * launch_gemv (v_dot4 path) on the repacked matrices. The reference plans
+ * this kernel (docs/kernel-design.md:53; block decode src/types.cpp:86-111)
+ * without building it. */
+int btf_hip_launch_gemv_ptq1_0(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, int mode,
+                               btf_stream_t stream);
+
 /* GEMV path policy: batches of M >= mfma_min_m rows run on the int8-MFMA
  * kernel, smaller ones on the v_dot4 kernel. 0 restores the default.
  * Process-global; for tests and benchmarks. Returns the previous value. */

@@ -115,6 +115,18 @@ inline void launch_gemv_ex(const GemvSeg* segs, int nseg, int K, int M, const Q8
                 "launch_gemv_ex");
 }
 
+// launch_gemv on PTQ1_0 matrices read directly (the native 1.75-bit GEMV the
+// reference plans in docs/kernel-design.md:53): GemvSeg::codes holds N rows
+// of K/128 28-byte PTQ1_0 blocks and GemvSeg::scales is nullptr.
+inline void launch_gemv_ptq1_0(const GemvSeg* segs, int nseg, int K, int M, const Q8Act& a, GemvMode mode,
+                               btf_stream_t st) {
+  if (nseg < 1 || nseg > 3) throw std::runtime_error("launch_gemv_ptq1_0: gemv: 1..3 segments");
+  btf_gemv_seg s[3] = {};
+  for (int i = 0; i < nseg; ++i) s[i] = btf_gemv_seg{segs[i].codes, segs[i].scales, segs[i].N, segs[i].y, segs[i].ldy};
+  const btf_q8act q{a.q, a.d, reinterpret_cast<int32_t*>(a.s)};
+  detail::check(btf_hip_launch_gemv_ptq1_0(s, nseg, K, M, &q, mode, st), "launch_gemv_ptq1_0");
+}
+
 // ---- the decode-step program (no counterpart in kernels.cuh: it replaces
 // the per-step graph of GEMV launches, src/cuda/gpu_decoder.cu:452-486)
 class StepProgram {

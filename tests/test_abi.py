@@ -96,6 +96,20 @@ def test_invalid_arguments_rejected_on_host():
     assert ex([seg, seg], 2, 1024, 1, act, None, 0, 0, act) == ARGS            # out: one segment
     assert ex([seg], 1, 1024, 1, act, None, 0, 0, h.Q8Act(0x400001, 0x500000, 0x600000)) == ARGS  # out align
     assert ex([seg], 1, 1024, 0, None, xa, 1024, 0) == h.BTF_OK                # M = 0: no-op
+    # PTQ1_0 GEMV: blocks carry their scales (scales must be NULL), 4-byte alignment, K <= 32768
+    b3 = h.launch_gemv_ptq1_0_raw
+    pseg = h.GemvSeg(codes + 4, None, 64, y, 64)
+    assert b3([h.GemvSeg(codes, scales, 64, y, 64)], 1, 1024, 1, act, 0) == ARGS  # scales given
+    assert "NULL" in h.last_error()
+    assert b3([h.GemvSeg(codes + 2, None, 64, y, 64)], 1, 1024, 1, act, 0) == ARGS  # block alignment
+    assert b3([pseg], 1, 1000, 1, act, 0) == ARGS                                 # K % 128
+    assert b3([pseg], 1, 32768 + 128, 1, act, 0) == ARGS                          # K too large
+    assert b3([pseg], 1, 1024, 1, act, 2) == ARGS                                 # swiglu needs 2 segs
+    assert b3([h.GemvSeg(codes, None, 64, None, 64)], 1, 1024, 1, act, 0) == ARGS  # null y
+    assert b3([h.GemvSeg(None, None, 64, y, 64)], 1, 1024, 1, act, 0) == ARGS     # null blocks
+    assert b3([pseg], 1, 1024, 1, h.Q8Act(0x400001, 0x500000, 0x600000), 0) == ARGS  # q alignment
+    assert b3([pseg], 1, 1024, 0, act, 0) == h.BTF_OK                             # M = 0: no-op
+    assert b3([pseg], 1, 1024, 1, act, 0) == h.BTF_ERR_NOT_INIT                   # valid: needs a device
     # decode-step ends: embedding lookup, greedy pick, position counter
     tok = 0x800000
     assert h.launch_embed_raw(codes, scales, tok, 1, 1000, None, y) == ARGS                 # E % 128
