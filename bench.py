@@ -633,7 +633,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this build runs on one GPU only: the ternary matmul path has no "
-                                   "multi-GPU code (see DESIGN.md for how it would shard)",
+                                   "multi-GPU code (a GPU would take a row share of every matrix; the design "
+                                   "is written up beside the code)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
