@@ -125,6 +125,18 @@ __device__ __forceinline__ uint32_t ctl_load(const uint32_t* p) {
 // never for its global loads (the weight stream stays in flight).
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// A compute wave's share of a GEMV op (its OpWork, below), computed by an
+// I/O wave one op ahead with one lane per compute wave and staged here: the
+// ten compute waves would otherwise each run the same scalar code at every
+// op boundary, on the one scalar issue slot of each SIMD.
+struct WorkRec {
+  int t0, n, P, uq;  // uq = u0 | s0 << 8 | q0 << 16
+};
+struct OpRec {
+  int first, R, next, sq;  // sq = S | qlog << 8
+};
+constexpr int kRecSlots = 3;  // records of ops i, i + 1, i + 2 (slot = op index % 3)
+
 struct Lds {
   OpDev opd[kMaxOps];        // the program
   uint32_t act_q[2][kMaxK / 4];  // q bytes of an op's input (by op parity)
@@ -134,6 +146,8 @@ struct Lds {
   float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
   uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
   uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
+  WorkRec wrec[kRecSlots][kCW];
+  OpRec orec[kRecSlots];
   uint32_t epoch;
   uint32_t abort_;
   uint32_t spin_max;
@@ -305,7 +319,9 @@ typedef const __attribute__((address_space(1))) _Float16 gf16;
 // 32*(j >> 4) + (j & 15), up row j 16 further).
 struct Slot {
   u32x4 c;
-  _Float16 s;  // fp16 scale of the chunk's 128-column block
+  uint32_t s;  // the aligned word holding the fp16 scale of the chunk's 128-column block (a
+               // full word: the compiler cannot pack two slots' scales into one register,
+               // which would make it wait for a refill right after issuing it)
 };
 
 // The items of an op are cut into batches of kRing, and each compute wave
@@ -323,7 +339,7 @@ struct OpWork {
 };
 // Every field is assigned on every path (a partly assigned struct would be
 // kept in scratch memory, whose accesses count in vmcnt).
-__device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int wg, int G, int i) {
+__device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave, int wg, int G, int i) {
   OpWork w;
   const bool past = i >= nops;
   const OpDev& o = L.opd[past ? 0 : i];
@@ -358,6 +374,38 @@ __device__ __forceinline__ OpWork op_work(const Lds& L, int nops, int wave, int 
   w.u0 = ua;
   w.s0 = ra >> w.qlog;
   w.q0 = ra & (Qu - 1);
+  return w;
+}
+
+// Stage the records of op i (lanes 0 .. kCW-1 of the first I/O wave, one
+// per compute wave); read by the compute waves after the next barrier B.
+__device__ __forceinline__ void stage_work(Lds& L, int nops, int wg, int G, int i, int iol) {
+  if (iol < kCW) {
+    const OpWork w = op_work_calc(L, nops, iol, wg, G, i);
+    const int slot = i % kRecSlots;
+    L.wrec[slot][iol] = WorkRec{w.t0, w.n, w.P, w.u0 | (w.s0 << 8) | (w.q0 << 16)};
+    if (iol == 0) L.orec[slot] = OpRec{w.first, w.R, w.next, w.S | (w.qlog << 8)};
+  }
+}
+__device__ __forceinline__ OpWork op_work(const Lds& L, int wave, int i) {
+  const int slot = i % kRecSlots;
+  const WorkRec& r = L.wrec[slot][wave];
+  const OpRec& o = L.orec[slot];
+  OpWork w;
+  w.i = i;
+  w.t0 = sgpr(r.t0);
+  w.n = sgpr(r.n);
+  w.P = sgpr(r.P);
+  const int uq = sgpr(r.uq);
+  w.u0 = uq & 255;
+  w.s0 = (uq >> 8) & 255;
+  w.q0 = uq >> 16;
+  w.first = sgpr(o.first);
+  w.R = sgpr(o.R);
+  w.next = sgpr(o.next);
+  const int sq = sgpr(o.sq);
+  w.S = sq & 255;
+  w.qlog = sq >> 8;
   return w;
 }
 
@@ -424,7 +472,7 @@ struct LaneOff {
   uint32_t c, s;
 };
 __device__ __forceinline__ LaneOff lane_off(const OpLd& d, int l16, int grp) {
-  return LaneOff{(uint32_t)grp * d.rowc + (uint32_t)l16 * 16u, (uint32_t)grp * d.rows + (uint32_t)(l16 >> 1) * 2u};
+  return LaneOff{(uint32_t)grp * d.rowc + (uint32_t)l16 * 16u, (uint32_t)grp * d.rows + (uint32_t)(l16 >> 2) * 4u};
 }
 
 // Position of a batch in the op's items: local unit, slice, first quad.
@@ -466,8 +514,7 @@ __device__ __forceinline__ void issue_entry(const OpLd& d, const LaneOff& lo, co
   const uint32_t oc = min(a.oc + dr * d.rowc, a.mc);
   const uint32_t os = min(a.os + dr * d.rows, a.ms);
   sl.c = __builtin_amdgcn_raw_buffer_load_b128(hi ? d.chi : d.clo, (int)lo.c, (int)oc, kNT);
-  const uint16_t h = __builtin_amdgcn_raw_buffer_load_b16(hi ? d.shi : d.slo, (int)lo.s, (int)os, kNT);
-  __builtin_memcpy(&sl.s, &h, 2);
+  sl.s = __builtin_amdgcn_raw_buffer_load_b32(hi ? d.shi : d.slo, (int)lo.s, (int)os, kNT);
 }
 
 // The activation of this lane's chunk of slice s: 64 q bytes, and per
@@ -531,10 +578,11 @@ struct Consumed {
   int y0, y1;
   float f;
 };
-__device__ __forceinline__ Consumed consume(const Slot& sl, const uint32_t (&aq)[16], const int (&an)[2]) {
+// hsh: 16 for a lane whose scale is the high half of its word (odd 128-column block), else 0
+__device__ __forceinline__ Consumed consume(const Slot& sl, uint32_t hsh, const uint32_t (&aq)[16], const int (&an)[2]) {
   Consumed r;
   const u32x4 wv = sl.c;
-  r.f = (float)sl.s;
+  r.f = h2f((uint16_t)(sl.s >> hsh));
   chunk_dot16(wv, aq, an, r.y0, r.y1);
   asm volatile("" : "+v"(r.f), "+v"(r.y0), "+v"(r.y1));
   return r;
@@ -592,8 +640,9 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
   const int l16 = lane & 15, grp = lane >> 4;
   const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
   const bool sum_lane = sum_lanes(l16);
+  const uint32_t hsh = (uint32_t)((l16 >> 1) & 1) * 16u;
   Slot ring[kRing];
-  OpWork cur = op_work(L, nops, wave, wg, G, first);
+  OpWork cur = op_work(L, wave, first);
   OpLd ld_cur = op_ld(L, first);
   LaneOff lo_cur = lane_off(ld_cur, l16, grp);
   {
@@ -606,7 +655,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     OpLd ld_nxt = ld_cur;
     BAddr a_nxt;
     {
-      const OpWork nw = op_work(L, nops, wave, wg, G, cur.next);
+      const OpWork nw = op_work(L, wave, cur.next);
       if (cur.next < nops) ld_nxt = op_ld(L, cur.next);
       a_nxt = batch_addr(ld_nxt, nw.first, G, BPos{nw.u0, nw.s0, nw.q0});
     }
@@ -653,7 +702,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
       float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
-        const Consumed c = consume(ring[r], aq, an);
+        const Consumed c = consume(ring[r], hsh, aq, an);
         __builtin_amdgcn_sched_barrier(0);
         issue_entry(ld, lo, a, r, ring[r]);
         __builtin_amdgcn_sched_barrier(0);
@@ -680,7 +729,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     }
     lds_barrier();  // B: every wave is done with the op
     if (cur.next >= nops) break;
-    cur = op_work(L, nops, wave, wg, G, cur.next);
+    cur = op_work(L, wave, cur.next);
     ld_cur = ld_nxt;
     lo_cur = lo_nxt;
   }
@@ -833,6 +882,8 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       continue;
     }
     const int nx = sgpr(op.next);
+    // the compute waves read op nx + 1's records at their next loop top (after B of this op)
+    stage_work(L, nops, wg, G, nx < nops ? sgpr(L.opd[nx].next) : nx + 1, iol);
     const bool early = nx < nops && sgpr(L.opd[nx].early);
     EarlyFetch ef;
     bool early_done = !early;
@@ -873,6 +924,12 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
     __hip_atomic_store(&L.abort_, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the staged words have landed
+  lds_barrier();
+  if (wave == kCW) {  // the compute waves' records of the first two GEMV ops
+    const int f2 = first_gemv < nops ? sgpr(L.opd[first_gemv].next) : first_gemv + 1;
+    stage_work(L, nops, wg, G, first_gemv, lane);
+    stage_work(L, nops, wg, G, f2, lane);
+  }
   lds_barrier();
   const uint32_t base_tag = L.epoch * (uint32_t)(nops + 1);
 
