@@ -56,6 +56,12 @@ struct B3Args {
   int m0, nb;
 };
 
+// k*v in each 16-bit lane
+__device__ __forceinline__ uint32_t mulk(uint32_t v, uint16_t k) {
+  u16x2 x = __builtin_bit_cast(u16x2, v);
+  x = x * k;
+  return __builtin_bit_cast(uint32_t, x);
+}
 // t = 3*v in each 16-bit lane
 __device__ __forceinline__ uint32_t mul3(uint32_t v) {
   u16x2 x = __builtin_bit_cast(u16x2, v);
@@ -67,36 +73,62 @@ __device__ __forceinline__ uint32_t mul3(uint32_t v) {
 __device__ __forceinline__ uint32_t spread_lo(uint32_t w) { return __builtin_amdgcn_perm(0u, w, 0x0c020c00u); }
 __device__ __forceinline__ uint32_t spread_hi(uint32_t w) { return __builtin_amdgcn_perm(0u, w, 0x0c030c01u); }
 
+// Digit n of a byte b is H(n+1) - 3*H(n), H(n) = floor(b * 3^n / 256) (the
+// high byte of b * 3^n, b * 3^5 < 2^16; H(0) = 0): the reference's
+// ((u8)(b*3^n) * 3) >> 8 is the carry out of the base-3 shift, and b * 3^n =
+// 256 * H(n) + (u8)(b*3^n). So for four bytes, with H(n) gathered into one
+// word (the high bytes of b * 3^n in two 16-bit-lane words, v_perm_b32),
+// sum_n digit_n . a_n = sum_n [H(n+1) . a_n - 3 * H(n) . a_n]: the products
+// are independent (no mask-and-multiply chain) and the -3 * H(n) terms go to
+// a second accumulator per sub-block. H(n) <= 80 for n <= 4 (a signed dot4
+// operand); H(5) <= 242 is not, so digit 4 is formed as bytes H(5) - 3*H(4)
+// (no carry: 3*H(4) <= 240, the difference is 0..2).
+struct Acc {
+  int a[4];  // sum of H(n+1) . a_n (and digit-4 / tail terms), starting at -s
+  int b[4];  // sum of H(n) . a_n, taken 3 times at the end
+};
+// Bytes of one word w (elements e(n, i) for digit n of byte i): the five
+// digit words dot the activation words act[n] (n = 0..4), into sub-blocks sb[n].
+__device__ __forceinline__ void word_dot(uint32_t w, const uint32_t (&act)[5], const int (&sb)[5], Acc& c) {
+  const uint32_t lo = spread_lo(w), hi = spread_hi(w);  // bytes 0, 2 / 1, 3 in 16-bit lanes
+  uint32_t H[6];
+#pragma unroll
+  for (int n = 1; n <= 5; ++n) {
+    constexpr uint16_t p3[6] = {1, 3, 9, 27, 81, 243};
+    const uint32_t pl = mulk(lo, p3[n]), ph = mulk(hi, p3[n]);  // b * 3^n, independent of each other
+    H[n] = __builtin_amdgcn_perm(ph, pl, 0x07030501u);           // high bytes: bytes 0, 1, 2, 3
+  }
+  // digits 0..3: H(n+1) . a_n - 3 H(n) . a_n
+#pragma unroll
+  for (int n = 0; n < 4; ++n) {
+    c.a[sb[n]] = sdot4(H[n + 1], act[n], c.a[sb[n]]);
+    if (n > 0) c.b[sb[n]] = sdot4(H[n], act[n], c.b[sb[n]]);
+  }
+  // digit 4 as bytes
+  const uint32_t d4 = H[5] - (H[4] + (H[4] << 1));
+  c.a[sb[4]] = sdot4(d4, act[4], c.a[sb[4]]);
+}
+
 // Sub-block sums I[k] = sum over the block's sub-block k of (digit - 1) * q,
 // from the block's 7 words w and its activation words a[0..31] (element 4i..
 // 4i+3 in a[i]); I[k] starts at -s[k].
 __device__ __forceinline__ void block_dot(const uint32_t (&w)[7], const uint32_t* a, int (&I)[4]) {
+  Acc c;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c.a[k] = I[k], c.b[k] = 0;
   // bytes 0..15: digit n of bytes 4g..4g+3 = elements 16n+4g.. -> word 4n+g, sub-block n/2
 #pragma unroll
   for (int g = 0; g < 4; ++g) {
-    uint32_t lo = spread_lo(w[g]), hi = spread_hi(w[g]);
-#pragma unroll
-    for (int n = 0; n < 5; ++n) {
-      const uint32_t tl = mul3(lo), th = mul3(hi);
-      const uint32_t tr = __builtin_amdgcn_perm(th, tl, 0x07030501u);  // high bytes: j, j+1, j+2, j+3
-      I[n >> 1] = sdot4(tr, a[4 * n + g], I[n >> 1]);
-      lo = tl & 0x00ff00ffu;
-      hi = th & 0x00ff00ffu;
-    }
+    const uint32_t act[5] = {a[g], a[4 + g], a[8 + g], a[12 + g], a[16 + g]};
+    const int sb[5] = {0, 0, 1, 1, 2};
+    word_dot(w[g], act, sb, c);
   }
   // bytes 16..23: digit n of bytes 16+4g.. = elements 80+8n+4g.. -> word 20+2n+g, sub-block (80+8n)/32
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    uint32_t lo = spread_lo(w[4 + g]), hi = spread_hi(w[4 + g]);
-#pragma unroll
-    for (int n = 0; n < 5; ++n) {
-      const uint32_t tl = mul3(lo), th = mul3(hi);
-      const uint32_t tr = __builtin_amdgcn_perm(th, tl, 0x07030501u);
-      const int k = n < 2 ? 2 : 3;
-      I[k] = sdot4(tr, a[20 + 2 * n + g], I[k]);
-      lo = tl & 0x00ff00ffu;
-      hi = th & 0x00ff00ffu;
-    }
+    const uint32_t act[5] = {a[20 + g], a[22 + g], a[24 + g], a[26 + g], a[28 + g]};
+    const int sb[5] = {2, 2, 3, 3, 3};
+    word_dot(w[4 + g], act, sb, c);
   }
   // bytes 24, 25: digits 0..3, elements 120+2n, 121+2n -> words 30, 31, sub-block 3
   uint32_t x = __builtin_amdgcn_perm(0u, w[6], 0x0c010c00u);  // byte 24 | byte 25 << 16
@@ -106,8 +138,10 @@ __device__ __forceinline__ void block_dot(const uint32_t (&w)[7], const uint32_t
     t[n] = mul3(x);
     x = t[n] & 0x00ff00ffu;
   }
-  I[3] = sdot4(__builtin_amdgcn_perm(t[1], t[0], 0x07050301u), a[30], I[3]);
-  I[3] = sdot4(__builtin_amdgcn_perm(t[3], t[2], 0x07050301u), a[31], I[3]);
+  c.a[3] = sdot4(__builtin_amdgcn_perm(t[1], t[0], 0x07050301u), a[30], c.a[3]);
+  c.a[3] = sdot4(__builtin_amdgcn_perm(t[3], t[2], 0x07050301u), a[31], c.a[3]);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) I[k] = c.a[k] - 3 * c.b[k];
 }
 
 template <int NB, int T, int R, int MODE>
