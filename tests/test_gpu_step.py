@@ -244,6 +244,36 @@ def test_step_each_op_vs_oracle(hip, oracle):
     prog.close()
 
 
+@pytest.mark.parametrize("nops", [1, 2])
+def test_step_one_and_two_ops(hip, oracle, nops):
+    """The shortest programs (the work records staged for ops past the end),
+    launched twice, bit-exact against the op-by-op launches."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(50 + nops)
+    W = [host_mat(oracle, rng, 2048, 1024), host_mat(oracle, rng, 1024, 2048)]
+    x0 = rng.standard_normal(1024).astype(np.float32)
+    r0 = rng.standard_normal(1024).astype(np.float32)
+    ops = [hip.StepGemv(G.kStore, 1024, 2048, W[0].codes, W[0].scales, 0, 1),
+           hip.StepGemv(G.kAdd, 2048, 1024, W[1].codes, W[1].scales, 1, 2)][:nops]
+
+    def vectors():
+        t = [dev(x0), torch.zeros(2048, dtype=torch.float32, device="cuda"), dev(r0)]
+        return [hip.StepVec(int(v.numel()), v) for v in t], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    _, s = vectors()
+    for rep in range(2):
+        prog.launch(stream())
+        run_sequential(hip, ops, s)
+        _torch().cuda.synchronize()
+        assert prog.error() == 0
+        for name, a, b in zip(("x", "a", "r"), t, s):
+            assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32)), f"launch {rep}: {name}"
+    prog.close()
+
+
 def test_step_repeated_launches(hip, oracle):
     """Three launches in a row continue the residual stream (the program's
     epoch/tag progression): equal to three sequential passes."""
