@@ -412,3 +412,18 @@ def test_embed_and_argmax_vs_reference_random(oracle, ref):
         if n > 10:
             l[[3, n - 2]] = l.max() + 1
         assert oracle.argmax(l) == ref.argmax(l)
+
+
+def test_base3_digit_identity_of_the_direct_gemv():
+    """The PTQ1_0-direct GEMV (csrc/gemv_b3.hip) forms digit n of a block byte
+    b as H(n+1) - 3 H(n), H(n) = floor(b 3^n / 256), instead of the
+    reference's ((u8)(b 3^n) * 3) >> 8 (src/types.hpp:70-78): equal for every
+    byte and digit, with the operand bounds the kernel relies on (b 3^5 fits
+    16-bit lanes, H(n) <= 80 for n <= 4 is a signed dot4 operand, 3 H(4)
+    fits a byte)."""
+    for b in range(256):
+        H = [(b * 3 ** n) >> 8 for n in range(6)]
+        assert b * 3 ** 5 < 1 << 16 and max(H[:5]) <= 80 and 3 * H[4] <= 240
+        for n in range(5):
+            ref = (((b * 3 ** n) & 0xFF) * 3) >> 8
+            assert ref == H[n + 1] - 3 * H[n], (b, n)
