@@ -511,14 +511,16 @@ def run_load(args, hip, torch):
     with open(path, "rb") as f:  # into the page cache
         while f.read(1 << 26):
             pass
-    arena, times, plan = None, [], None
+    arena, times, plan, phases = None, [], None, []
     for rep in range(args.warmup + args.steps):
         t0 = time.perf_counter()
         g = hip.Gguf(path)
         plan = g.plan(staging)
         if arena is None:
             arena = torch.empty(plan["arena_bytes"], dtype=torch.uint8, device="cuda")
+        t1 = time.perf_counter()
         L = hip.Loader(staging)
+        t2 = time.perf_counter()
         st = torch.cuda.current_stream().cuda_stream
         off, base = 0, arena.data_ptr()
         for t in g.tensors:
@@ -537,7 +539,11 @@ def run_load(args, hip, torch):
         assert n == plan["source_bytes"] == src_bytes
         if rep >= args.warmup:
             times.append(dt)
+            phases.append((t1 - t0, t2 - t1, dt - (t2 - t0)))
     t = float(np.median(times))
+    ph = np.median(np.array(phases), axis=0)
+    log(f"load phases (median): open + plan {ph[0] * 1e3:.2f} ms, loader (pinned + device staging) "
+        f"{ph[1] * 1e3:.2f} ms, uploads + finish {ph[2] * 1e3:.2f} ms")
     value = src_bytes / t / 1e9
     log(f"load: {t * 1e3:.1f} ms for {src_bytes / 1e9:.3f} GB of PTQ1_0 -> {plan['arena_bytes'] / 1e9:.3f} GB "
         f"resident: {value:.2f} GB/s")
@@ -605,6 +611,8 @@ def run_load(args, hip, torch):
                    "parallelism": "single GPU"},
         "stages_gbs": {"host_copy": round(host_gbs, 2), "copy_engine": round(dma_gbs, 2),
                        "repack_kernel": round(rep_gbs, 1)},
+        "phases_ms": {"open_plan": round(ph[0] * 1e3, 2), "loader_create": round(ph[1] * 1e3, 2),
+                      "uploads": round(ph[2] * 1e3, 2)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

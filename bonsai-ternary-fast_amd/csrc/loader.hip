@@ -8,7 +8,8 @@
 // whole rows through two pinned staging slots in turn; before a slot is
 // refilled the host waits for the event recorded after its previous slice's
 // repack, so the host's copy of one slice overlaps the device's work on the
-// other. The host copy of a slice runs on up to 8 threads. The reference's
+// other. The host copy of a slice runs on a pool of up to 16 threads started
+// with the loader. The reference's
 // repack kernel reads a mapped pinned slot across the bus; here each slice is
 // instead copied by the DMA engine into a device staging slot
 // (hipMemcpyAsync) and repacked from HBM, so the repack kernel never runs at
@@ -23,7 +24,9 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <condition_variable>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <thread>
 #include <vector>
@@ -33,6 +36,79 @@
 
 namespace btfhip {
 
+// Worker threads for the host copy of a slice, started once with the loader:
+// a slice is cut into parts of at least 1 MiB, part 0 copied by the calling
+// thread and part t by worker t - 1 (one thread copies a page-cache mapping
+// at ~10 GB/s; the copy engine moves ~55 GB/s).
+struct CopyPool {
+  std::vector<std::thread> workers;
+  std::mutex mu;
+  std::condition_variable go, done;
+  uint64_t gen = 0;  // job number
+  int pending = 0;   // workers still copying the current job
+  bool stop = false;
+  char* dst = nullptr;
+  const char* src = nullptr;
+  size_t bytes = 0, part = 0;
+  int nparts = 0;
+
+  void run(int t) {  // worker t copies part t + 1
+    uint64_t seen = 0;
+    for (;;) {
+      std::unique_lock<std::mutex> lk(mu);
+      go.wait(lk, [&] { return stop || gen != seen; });
+      if (stop) return;
+      seen = gen;
+      const int k = t + 1;
+      const bool mine = k < nparts;
+      char* d = dst;
+      const char* sp = src;
+      const size_t b = std::min(bytes, (size_t)k * part), e = std::min(bytes, (size_t)(k + 1) * part);
+      lk.unlock();
+      if (mine && e > b) std::memcpy(d + b, sp + b, e - b);
+      lk.lock();
+      if (--pending == 0) done.notify_one();
+    }
+  }
+  void start(int n) {  // fewer workers if the system refuses threads
+    try {
+      for (int t = 0; t < n; ++t) workers.emplace_back([this, t] { run(t); });
+    } catch (const std::exception&) {
+    }
+  }
+  void copy(void* d, const void* sp, size_t n_bytes) {
+    const size_t min_part = (size_t)1 << 20;
+    const int n = (int)std::max<size_t>(1, std::min<size_t>(workers.size() + 1, n_bytes / min_part));
+    if (n == 1) {
+      std::memcpy(d, sp, n_bytes);
+      return;
+    }
+    const size_t p = (n_bytes / n + 4095) & ~(size_t)4095;
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      dst = static_cast<char*>(d);
+      src = static_cast<const char*>(sp);
+      bytes = n_bytes;
+      part = p;
+      nparts = n;
+      pending = (int)workers.size();
+      ++gen;
+    }
+    go.notify_all();
+    std::memcpy(d, sp, std::min(n_bytes, p));
+    std::unique_lock<std::mutex> lk(mu);
+    done.wait(lk, [&] { return pending == 0; });
+  }
+  ~CopyPool() {
+    {
+      std::lock_guard<std::mutex> lk(mu);
+      stop = true;
+    }
+    go.notify_all();
+    for (std::thread& th : workers) th.join();
+  }
+};
+
 struct Loader {
   int device = 0;
   size_t slot_bytes = 0;
@@ -41,29 +117,8 @@ struct Loader {
   hipEvent_t ev[2] = {nullptr, nullptr};
   int slot = 0;
   uint64_t source_bytes = 0;  // PTQ1_0 bytes uploaded so far
-  int threads = 1;            // host threads per slice copy
+  CopyPool pool;              // host copy of a slice
 };
-
-// The host copy of a slice, split over L->threads threads in chunks of at
-// least 4 MiB (one thread copies a page-cache mapping at ~10 GB/s; the copy
-// engine moves ~56 GB/s).
-static void copy_slice(const Loader* L, void* dst, const void* src, size_t bytes) {
-  const size_t min_chunk = (size_t)4 << 20;
-  const int n = (int)std::max<size_t>(1, std::min<size_t>((size_t)L->threads, bytes / min_chunk));
-  if (n == 1) {
-    std::memcpy(dst, src, bytes);
-    return;
-  }
-  const size_t part = (bytes / n + 4095) & ~(size_t)4095;
-  std::vector<std::thread> pool;
-  for (int t = 1; t < n; ++t) {
-    const size_t b = std::min(bytes, (size_t)t * part), e = std::min(bytes, (size_t)(t + 1) * part);
-    if (e > b)
-      pool.emplace_back([=] { std::memcpy(static_cast<char*>(dst) + b, static_cast<const char*>(src) + b, e - b); });
-  }
-  std::memcpy(dst, src, std::min(bytes, part));
-  for (std::thread& th : pool) th.join();
-}
 
 static void loader_free(Loader* L) {
   for (int i = 0; i < 2; ++i) {
@@ -90,7 +145,6 @@ int btf_hip_loader_create(uint64_t staging_bytes, btf_loader_t* out) {
   if (!ds) return BTF_ERR_NOT_INIT;
   Loader* L = new Loader();
   (void)hipGetDevice(&L->device);
-  L->threads = (int)std::max(1u, std::min(8u, std::thread::hardware_concurrency()));
   L->slot_bytes = (size_t)staging_bytes;
   for (int i = 0; i < 2; ++i) {
     if (hipHostMalloc(&L->host[i], L->slot_bytes, hipHostMallocDefault) != hipSuccess ||
@@ -100,6 +154,7 @@ int btf_hip_loader_create(uint64_t staging_bytes, btf_loader_t* out) {
       return fail(BTF_ERR_LAUNCH, "loader: staging allocation failed");
     }
   }
+  L->pool.start((int)std::max(1u, std::min(16u, std::thread::hardware_concurrency())) - 1);
   *out = L;
   return BTF_OK;
 }
@@ -130,7 +185,7 @@ int btf_hip_loader_upload_ptq1_0(btf_loader_t h, const uint8_t* src, int64_t N, 
     L->slot ^= 1;
     // the slot's previous slice has been copied and repacked
     if (hipEventSynchronize(L->ev[s]) != hipSuccess) return fail(BTF_ERR_LAUNCH, "loader: staging wait failed");
-    btfhip::copy_slice(L, L->host[s], src + (size_t)r0 * row_bytes, bytes);
+    L->pool.copy(L->host[s], src + (size_t)r0 * row_bytes, bytes);
     if (hipMemcpyAsync(L->dev[s], L->host[s], bytes, hipMemcpyHostToDevice, st) != hipSuccess)
       return fail(BTF_ERR_LAUNCH, "loader: staging copy failed");
     const int rc = btfhip::repack(static_cast<const uint8_t*>(L->dev[s]), rows * nb, codes + r0 * (K / 4),
