@@ -353,19 +353,22 @@ __device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave,
   w.R = (nunits << w.qlog) * 4;
   const int U = w.S << w.qlog;  // items per unit
   const int T = nunits * U;
-  // Batches are balanced over the four SIMDs, not over the waves: wave w
-  // sits on SIMD w % 4, SIMDs 0 and 1 hold three compute waves and SIMDs 2
-  // and 3 two (beside the I/O waves), and a SIMD's waves mostly run one after
-  // another (the oldest issues first), so an op ends when its busiest SIMD
-  // does. SIMD k takes B/4 batches (the first B % 4 SIMDs one more), split
-  // over its waves the same way; runs follow in SIMD-major wave order.
+  // Batches are spread evenly over the waves, floor(B / kCW) each, the
+  // remaining B % kCW one more each, those first to the waves of SIMDs 2 and
+  // 3 (two compute waves each, beside the I/O waves; SIMDs 0 and 1 hold
+  // three): a wave's batches are rounds of its ring (each waits for the
+  // loads issued during the previous one), so the op takes as many rounds
+  // as its busiest wave has batches. Runs follow in wave order.
+  static_assert(kCW == 10, "the extra-batch order below assumes 3 + 3 + 2 + 2 compute waves per SIMD");
   const int B = (T + kRing - 1) / kRing;
-  const int simd = wave & 3, slot = wave >> 2;         // slot: the wave's rank on its SIMD
-  const int nws = simd < kCW - 8 ? 3 : 2;              // compute waves on this SIMD
-  const int bs = B / 4 + (simd < B % 4 ? 1 : 0);       // batches of this SIMD
-  const int sb0 = simd * (B / 4) + (simd < B % 4 ? simd : B % 4);  // its first batch
-  const int b0 = sb0 + slot * (bs / nws) + (slot < bs % nws ? slot : bs % nws);
-  const int b1 = b0 + bs / nws + (slot < bs % nws ? 1 : 0);
+  const int base = B / kCW, extra = B % kCW;
+  auto xrank = [](int v) {  // order of the extra batches: waves 2, 3, 6, 7, then 0, 1, 4, 5, 8, 9
+    const int sm = v & 3, sl = v >> 2;
+    return sm >= 2 ? (sm - 2) + 2 * sl : 4 + sm + 2 * sl;
+  };
+  int b0 = base * wave;
+  for (int v = 0; v < wave; ++v) b0 += xrank(v) < extra ? 1 : 0;
+  const int b1 = b0 + base + (xrank(wave) < extra ? 1 : 0);
   w.t0 = b0 * kRing;
   const int t1 = b1 * kRing < T ? b1 * kRing : T;
   w.n = t1 > w.t0 ? t1 - w.t0 : 0;
