@@ -818,7 +818,7 @@ def main():
             roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
                     "traffic_source": tr["source"] if tr else None,
-                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 3 else 'gemm_mfma_kernel'}"
+                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 5 else 'gemm_mfma_kernel'}"
                               f"{', quantizes fused in' if fk else ''})",
                     "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
         else:

@@ -49,17 +49,19 @@ struct MfmaArgs {
   int32_t* dump;
 };
 
-constexpr int kCodeStride = 9;  // words per staged code row (32 B + 4 B pad)
-
-template <int MT, int MODE, bool DUMP>
+// KB 128-column blocks are staged per iteration (one round of loads per KB
+// blocks instead of per block: the loop is bound by load latency, not by
+// the MFMA work of a block).
+template <int MT, int KB, int MODE, bool DUMP>
 __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
   constexpr int BM = 16 * MT;
-  constexpr int QS = 34;  // words per staged q row (128 B + 8 B pad)
-  __shared__ uint32_t cs[64 * kCodeStride];
-  __shared__ uint16_t scs[64];
+  constexpr int CS = 8 * KB + 1;   // words per staged code row (KB x 32 B + 4 B pad)
+  constexpr int QS = 32 * KB + 2;  // words per staged q row (KB x 128 B + 8 B pad)
+  __shared__ uint32_t cs[64 * CS];
+  __shared__ uint16_t scs[64 * KB];
   __shared__ uint32_t qsm[BM * QS];
-  __shared__ float dsm[4][BM];
-  __shared__ int32_t nsm[4][BM];
+  __shared__ float dsm[4 * KB][BM];
+  __shared__ int32_t nsm[4 * KB][BM];
   __shared__ float upx[(MODE == BTF_GEMV_SWIGLU) ? 32 * BM : 1];
 
   const int tid = threadIdx.x;
@@ -90,37 +92,46 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.f;
 
-  for (int kb = 0; kb < nsc; ++kb) {
-    // ---- stage the block ----
-    if (tid < 128) {
-      const int r = tid >> 1, half = tid & 1;
+  for (int kb0 = 0; kb0 < nsc; kb0 += KB) {
+    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;  // blocks this iteration
+    // ---- stage nkb blocks: codes (64 rows x 32 B each), scales, q, d / -s ----
+    for (int i = tid; i < 64 * 2 * KB; i += 256) {
+      const int r = i / (2 * KB), part = i - r * (2 * KB);  // part: 16-byte half of block part / 2
+      if (part >= 2 * nkb) continue;
       const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
       const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
       const int nc = nr < N ? nr : N - 1;
       const uint8_t* cb = up ? a.up_codes : codes;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb * 32 + 16 * half);
-      uint32_t* o = &cs[r * kCodeStride + 4 * half];
+      const u32x4 v = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
+      uint32_t* o = &cs[r * CS + 4 * part];
       o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-      if (half == 0) {
-        const uint16_t* sb = up ? a.up_scales : scales;
-        scs[r] = sb[(size_t)nc * nsc + kb];
-      }
     }
-    for (int i = tid; i < BM * 8; i += 256) {
-      const int r = i >> 3, part = i & 7;
+    for (int i = tid; i < 64 * KB; i += 256) {
+      const int r = i / KB, j = i - r * KB;
+      if (j >= nkb) continue;
+      const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
+      const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
+      const int nc = nr < N ? nr : N - 1;
+      const uint16_t* sb = up ? a.up_scales : scales;
+      scs[r * KB + j] = sb[(size_t)nc * nsc + kb0 + j];
+    }
+    for (int i = tid; i < BM * 8 * KB; i += 256) {
+      const int r = i / (8 * KB), part = i - r * (8 * KB);
+      if (part >= 8 * nkb) continue;
       const int m = mb + r;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < a.nb) v = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb * 128 + 16 * part);
+      if (m < a.nb) v = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
       uint32_t* o = &qsm[r * QS + 4 * part];
       o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
     }
-    for (int i = tid; i < BM * 4; i += 256) {
-      const int r = i >> 2, sb = i & 3;
+    for (int i = tid; i < BM * 4 * KB; i += 256) {
+      const int r = i / (4 * KB), sb = i - r * (4 * KB);
+      if (sb >= 4 * nkb) continue;
       const int m = mb + r;
       float dv = 0.f;
       int sv = 0;
       if (m < a.nb) {
-        const size_t o = (size_t)(a.m0 + m) * nsub + kb * 4 + sb;
+        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
         dv = a.d[o];
         sv = a.s[o];
       }
@@ -129,23 +140,26 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
     }
     __syncthreads();
 
+    for (int kbi = 0; kbi < nkb; ++kbi) {
+    const int kb = kb0 + kbi;
     // ---- 4 sub-blocks of MFMA ----
 #pragma unroll
     for (int sb = 0; sb < 4; ++sb) {
-      const uint32_t word = cs[(16 * w + li) * kCodeStride + 2 * sb + (t >> 1)];
+      const int sbx = 4 * kbi + sb;  // staged sub-block
+      const uint32_t word = cs[(16 * w + li) * CS + 2 * sbx + (t >> 1)];
       const int sh = 4 * (t & 1);
       const uint32_t lo = (word >> sh) & 0x03030303u;
       const uint32_t hi = (word >> (sh + 2)) & 0x03030303u;
       const long bfrag = (long)(((uint64_t)hi << 32) | lo);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const uint32_t* ap = &qsm[(16 * mt + li) * QS + 8 * sb + 2 * t];
+        const uint32_t* ap = &qsm[(16 * mt + li) * QS + 8 * sbx + 2 * t];
         const long afrag = (long)(((uint64_t)ap[1] << 32) | ap[0]);
         v4i cin;
-        cin[0] = nsm[sb][16 * mt + 4 * t + 0];
-        cin[1] = nsm[sb][16 * mt + 4 * t + 1];
-        cin[2] = nsm[sb][16 * mt + 4 * t + 2];
-        cin[3] = nsm[sb][16 * mt + 4 * t + 3];
+        cin[0] = nsm[sbx][16 * mt + 4 * t + 0];
+        cin[1] = nsm[sbx][16 * mt + 4 * t + 1];
+        cin[2] = nsm[sbx][16 * mt + 4 * t + 2];
+        cin[3] = nsm[sbx][16 * mt + 4 * t + 3];
         const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag, cin, 0, 0, 0);
         if constexpr (DUMP) {
           const int n = n0 + 16 * w + li;
@@ -157,19 +171,20 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
         } else {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
-            const float dv = dsm[sb][16 * mt + 4 * t + r];
+            const float dv = dsm[sbx][16 * mt + 4 * t + r];
             blk[mt][r] = sb == 0 ? dv * (float)I[r] : fmaf(dv, (float)I[r], blk[mt][r]);
           }
         }
       }
     }
     if constexpr (!DUMP) {
-      const float sc = h2f(scs[16 * w + li]);
+      const float sc = h2f(scs[(16 * w + li) * KB + kbi]);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, blk[mt][r], acc[mt][r]);
     }
+    }  // kbi
     __syncthreads();
   }
   if constexpr (DUMP) return;
@@ -217,12 +232,13 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
 
 template <int MT, bool DUMP>
 void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int KB = MT >= 4 ? 1 : 8;
   if (mode == BTF_GEMV_STORE)
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
   else if (mode == BTF_GEMV_ADD)
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, BTF_GEMV_ADD, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
 }
 
 }  // namespace

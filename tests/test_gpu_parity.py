@@ -344,7 +344,7 @@ def test_gemv_fused_input_quantize(hip, oracle, K, M):
                 segs = [hip.GemvSeg(dev(mat[0]), dev(mat[1]), N, y, N)]
             if fused:
                 hip.launch_gemv_ex(segs, K, M, x=xd, ldx=ldx, mode=mode, stream=stream())
-            else:  # on the v_dot4 path too (M >= 3 would take the MFMA kernel, another float order)
+            else:  # on the v_dot4 path too (larger M takes the MFMA kernel, another float order)
                 prev = hip.gemv_set_policy(1 << 20)
                 try:
                     hip.launch_gemv(segs, K, M, a, mode, stream())
