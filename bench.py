@@ -635,6 +635,8 @@ def main():
     ap.add_argument("--b3", dest="b3", action="store_true", default=None,
                     help="also time the chain on the PTQ1_0 rows read directly (default: with --engine auto)")
     ap.add_argument("--no-b3", dest="b3", action="store_false")
+    ap.add_argument("--mfma-min-m", type=int, default=0,
+                    help="batch rows from which GEMVs run on the int8 MFMA kernels (0: the library default)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run 3 device copies of 1 GiB (the scale reference for HBM counters)")
     args = ap.parse_args()
@@ -652,6 +654,8 @@ def main():
 
     torch.cuda.set_device(0)
     hip.kernels_init(0)
+    if args.mfma_min_m:
+        hip.gemv_set_policy(args.mfma_min_m)
     info = hip.device_info(0)
     log(f"device {info['name']} {info['gcn_arch']} CUs={info['cu_count']}")
 
@@ -818,7 +822,7 @@ def main():
             roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
                     "traffic_source": tr["source"] if tr else None,
-                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < 5 else 'gemm_mfma_kernel'}"
+                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < (args.mfma_min_m or 3) else 'gemm_ks_kernel'}"
                               f"{', quantizes fused in' if fk else ''})",
                     "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
         else:

@@ -19,7 +19,7 @@ constexpr int kMaxDevices = 64;
 DevState g_dev[kMaxDevices];
 std::mutex g_init_mu;
 // Batches of M >= this many rows use the int8-MFMA kernel.
-constexpr int kDefaultMfmaMinM = 5;
+constexpr int kDefaultMfmaMinM = 3;
 int g_mfma_min_m = kDefaultMfmaMinM;
 
 bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }

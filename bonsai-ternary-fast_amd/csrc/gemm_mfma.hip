@@ -92,53 +92,109 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) acc[mt][r] = 0.f;
 
+  // Software pipeline: the loads of the next KB blocks go to registers while
+  // the current ones are dotted from LDS; a thread's share of a stage is at
+  // most NCV/NSV/NQV/NDV vector, scale, q and d/s loads.
+  constexpr int NCV = (64 * 2 * KB + 255) / 256;  // 16-byte code loads
+  constexpr int NSV = (64 * KB + 255) / 256;      // scale loads
+  constexpr int NQV = (BM * 8 * KB + 255) / 256;  // 16-byte q loads
+  constexpr int NDV = (BM * 4 * KB + 255) / 256;  // d / s loads
+  u32x4 rc[NCV], rq[NQV];
+  uint16_t rsc[NSV];
+  float rd[NDV];
+  int rs[NDV];
+  auto fetch = [&](int kb0) {
+    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (2 * KB), part = i - r * (2 * KB);  // part: 16-byte half of block part / 2
+      rc[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < 64 * 2 * KB && part < 2 * nkb) {
+        const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
+        const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
+        const int nc = nr < N ? nr : N - 1;
+        const uint8_t* cb = up ? a.up_codes : codes;
+        rc[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / KB, jj = i - r * KB;
+      rsc[j] = 0;
+      if (i < 64 * KB && jj < nkb) {
+        const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
+        const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
+        const int nc = nr < N ? nr : N - 1;
+        const uint16_t* sb = up ? a.up_scales : scales;
+        rsc[j] = sb[(size_t)nc * nsc + kb0 + jj];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (8 * KB), part = i - r * (8 * KB);
+      const int m = mb + r;
+      rq[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < BM * 8 * KB && part < 8 * nkb && m < a.nb)
+        rq[j] = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (4 * KB), sb = i - r * (4 * KB);
+      const int m = mb + r;
+      rd[j] = 0.f;
+      rs[j] = 0;
+      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) {
+        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
+        rd[j] = a.d[o];
+        rs[j] = a.s[o];
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < 64 * 2 * KB) {
+        const int r = i / (2 * KB), part = i - r * (2 * KB);
+        uint32_t* o = &cs[r * CS + 4 * part];
+        o[0] = rc[j].x; o[1] = rc[j].y; o[2] = rc[j].z; o[3] = rc[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < 64 * KB) scs[(i / KB) * KB + (i - (i / KB) * KB)] = rsc[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < BM * 8 * KB) {
+        const int r = i / (8 * KB), part = i - r * (8 * KB);
+        uint32_t* o = &qsm[r * QS + 4 * part];
+        o[0] = rq[j].x; o[1] = rq[j].y; o[2] = rq[j].z; o[3] = rq[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < BM * 4 * KB) {
+        const int r = i / (4 * KB), sb = i - r * (4 * KB);
+        dsm[sb][r] = rd[j];
+        nsm[sb][r] = -rs[j];
+      }
+    }
+  };
+
+  fetch(0);
   for (int kb0 = 0; kb0 < nsc; kb0 += KB) {
     const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;  // blocks this iteration
-    // ---- stage nkb blocks: codes (64 rows x 32 B each), scales, q, d / -s ----
-    for (int i = tid; i < 64 * 2 * KB; i += 256) {
-      const int r = i / (2 * KB), part = i - r * (2 * KB);  // part: 16-byte half of block part / 2
-      if (part >= 2 * nkb) continue;
-      const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
-      const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
-      const int nc = nr < N ? nr : N - 1;
-      const uint8_t* cb = up ? a.up_codes : codes;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
-      uint32_t* o = &cs[r * CS + 4 * part];
-      o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-    }
-    for (int i = tid; i < 64 * KB; i += 256) {
-      const int r = i / KB, j = i - r * KB;
-      if (j >= nkb) continue;
-      const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
-      const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
-      const int nc = nr < N ? nr : N - 1;
-      const uint16_t* sb = up ? a.up_scales : scales;
-      scs[r * KB + j] = sb[(size_t)nc * nsc + kb0 + j];
-    }
-    for (int i = tid; i < BM * 8 * KB; i += 256) {
-      const int r = i / (8 * KB), part = i - r * (8 * KB);
-      if (part >= 8 * nkb) continue;
-      const int m = mb + r;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (m < a.nb) v = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
-      uint32_t* o = &qsm[r * QS + 4 * part];
-      o[0] = v.x; o[1] = v.y; o[2] = v.z; o[3] = v.w;
-    }
-    for (int i = tid; i < BM * 4 * KB; i += 256) {
-      const int r = i / (4 * KB), sb = i - r * (4 * KB);
-      if (sb >= 4 * nkb) continue;
-      const int m = mb + r;
-      float dv = 0.f;
-      int sv = 0;
-      if (m < a.nb) {
-        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
-        dv = a.d[o];
-        sv = a.s[o];
-      }
-      dsm[sb][r] = dv;
-      nsm[sb][r] = -sv;
-    }
+    stage();
     __syncthreads();
+    if (kb0 + KB < nsc) fetch(kb0 + KB);  // in flight while this stage is dotted
 
     for (int kbi = 0; kbi < nkb; ++kbi) {
     const int kb = kb0 + kbi;
@@ -230,6 +286,261 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
   }
 }
 
+// K-split tile for batched decode (up to 32 activation rows): a workgroup
+// owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows) and BM
+// activation rows, and wave w walks its quarter of the 128-column blocks,
+// staging its own codes, scales, q and d / -s in a private LDS region. Four
+// times as many workgroups as the 64-row tile and a quarter of the serial
+// MFMA chain per wave; the activation is re-read from L2 by each tile. Per
+// wave the row sums follow the 64-row kernel's order over its blocks, and the
+// four wave partials are added in wave order: ((p0 + p1) + p2) + p3.
+template <int MT, int KB, int MODE, bool DUMP>
+__global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
+  constexpr int BM = 16 * MT;
+  constexpr int G = MODE == BTF_GEMV_SWIGLU ? 2 : 1;  // 16-row groups: gate (and up)
+  constexpr int RW = 16 * G;                          // staged rows per wave
+  constexpr int CS = 8 * KB + 1;
+  constexpr int QS = 32 * KB + 2;
+  constexpr int NCV = (RW * 2 * KB + 63) / 64;  // per-lane 16-byte code loads
+  constexpr int NSV = (RW * KB + 63) / 64;      // scale loads
+  constexpr int NQV = (BM * 8 * KB + 63) / 64;  // 16-byte q loads
+  constexpr int NDV = (BM * 4 * KB + 63) / 64;  // d / s loads
+  __shared__ uint32_t cs[4][RW * CS];
+  __shared__ uint16_t scs[4][RW * KB];
+  __shared__ uint32_t qsm[4][BM * QS];
+  __shared__ float dsm[4][4 * KB][BM];
+  __shared__ int32_t nsm[4][4 * KB][BM];
+  static_assert(sizeof(qsm) >= 4 * G * 16 * BM * sizeof(float), "partials alias the q stage");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int li = lane & 15;
+  const int t = lane >> 4;
+
+  const int bx = blockIdx.x;
+  const int seg = (bx >= a.tile_start[1]) + (bx >= a.tile_start[2]);
+  const uint8_t* codes = seg == 0 ? a.codes[0] : seg == 1 ? a.codes[1] : a.codes[2];
+  const uint16_t* scales = seg == 0 ? a.scales[0] : seg == 1 ? a.scales[1] : a.scales[2];
+  float* y = seg == 0 ? a.y[0] : seg == 1 ? a.y[1] : a.y[2];
+  const int N = seg == 0 ? a.N[0] : seg == 1 ? a.N[1] : a.N[2];
+  const int ldy = seg == 0 ? a.ldy[0] : seg == 1 ? a.ldy[1] : a.ldy[2];
+  const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
+  const int K = a.K;
+  const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
+  const int n0 = (bx - tile0) * 16;
+  const int mb = blockIdx.y * BM;
+
+  // this wave's blocks [kw0, kw1); every wave runs niter iterations so the
+  // workgroup barriers match
+  const int kw0 = nsc * w / 4, kw1 = nsc * (w + 1) / 4;
+  const int niter = ((nsc + 3) / 4 + KB - 1) / KB;
+
+  float acc[G][MT][4], blk[G][MT][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[g][mt][r] = 0.f;
+
+  u32x4 rc[NCV], rq[NQV];
+  uint16_t rsc[NSV];
+  float rd[NDV];
+  int rs[NDV];
+  auto fetch = [&](int it) {
+    const int kb0 = kw0 + it * KB;
+    const int nkb = kw1 - kb0 < KB ? kw1 - kb0 : KB;  // may be <= 0 on the last iteration
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = lane + 64 * j;
+      const int r = i / (2 * KB), part = i - r * (2 * KB);
+      rc[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < RW * 2 * KB && part < 2 * nkb) {
+        const int nr = n0 + (r & 15);
+        const int nc = nr < N ? nr : N - 1;
+        const uint8_t* cb = r >= 16 ? a.up_codes : codes;
+        rc[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = lane + 64 * j;
+      const int r = i / KB, jj = i - r * KB;
+      rsc[j] = 0;
+      if (i < RW * KB && jj < nkb) {
+        const int nr = n0 + (r & 15);
+        const int nc = nr < N ? nr : N - 1;
+        const uint16_t* sb = r >= 16 ? a.up_scales : scales;
+        rsc[j] = sb[(size_t)nc * nsc + kb0 + jj];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = lane + 64 * j;
+      const int r = i / (8 * KB), part = i - r * (8 * KB);
+      const int m = mb + r;
+      rq[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < BM * 8 * KB && part < 8 * nkb && m < a.nb)
+        rq[j] = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = lane + 64 * j;
+      const int r = i / (4 * KB), sb = i - r * (4 * KB);
+      const int m = mb + r;
+      rd[j] = 0.f;
+      rs[j] = 0;
+      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) {
+        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
+        rd[j] = a.d[o];
+        rs[j] = a.s[o];
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < RW * 2 * KB) {
+        const int r = i / (2 * KB), part = i - r * (2 * KB);
+        uint32_t* o = &cs[w][r * CS + 4 * part];
+        o[0] = rc[j].x; o[1] = rc[j].y; o[2] = rc[j].z; o[3] = rc[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < RW * KB) scs[w][i] = rsc[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < BM * 8 * KB) {
+        const int r = i / (8 * KB), part = i - r * (8 * KB);
+        uint32_t* o = &qsm[w][r * QS + 4 * part];
+        o[0] = rq[j].x; o[1] = rq[j].y; o[2] = rq[j].z; o[3] = rq[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = lane + 64 * j;
+      if (i < BM * 4 * KB) {
+        const int r = i / (4 * KB), sb = i - r * (4 * KB);
+        dsm[w][sb][r] = rd[j];
+        nsm[w][sb][r] = -rs[j];
+      }
+    }
+  };
+
+  fetch(0);
+  for (int it = 0; it < niter; ++it) {
+    const int kb0 = kw0 + it * KB;
+    const int nkb = kw1 - kb0 < KB ? kw1 - kb0 : KB;
+    stage();
+    __syncthreads();
+    if (it + 1 < niter) fetch(it + 1);  // in flight while this stage is dotted
+
+    for (int kbi = 0; kbi < nkb; ++kbi) {
+      const int kb = kb0 + kbi;
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        const int sbx = 4 * kbi + sb;
+        long bfrag[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint32_t word = cs[w][(16 * g + li) * CS + 2 * sbx + (t >> 1)];
+          const int sh = 4 * (t & 1);
+          const uint32_t lo = (word >> sh) & 0x03030303u;
+          const uint32_t hi = (word >> (sh + 2)) & 0x03030303u;
+          bfrag[g] = (long)(((uint64_t)hi << 32) | lo);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const uint32_t* ap = &qsm[w][(16 * mt + li) * QS + 8 * sbx + 2 * t];
+          const long afrag = (long)(((uint64_t)ap[1] << 32) | ap[0]);
+          v4i cin;
+          cin[0] = nsm[w][sbx][16 * mt + 4 * t + 0];
+          cin[1] = nsm[w][sbx][16 * mt + 4 * t + 1];
+          cin[2] = nsm[w][sbx][16 * mt + 4 * t + 2];
+          cin[3] = nsm[w][sbx][16 * mt + 4 * t + 3];
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[g], cin, 0, 0, 0);
+            if constexpr (DUMP) {
+              const int n = n0 + li;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int m = mb + 16 * mt + 4 * t + r;
+                if (g == 0 && m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + kb * 4 + sb] = I[r];
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const float dv = dsm[w][sbx][16 * mt + 4 * t + r];
+                blk[g][mt][r] = sb == 0 ? dv * (float)I[r] : fmaf(dv, (float)I[r], blk[g][mt][r]);
+              }
+            }
+          }
+        }
+      }
+      if constexpr (!DUMP) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float sc = h2f(scs[w][(16 * g + li) * KB + kbi]);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[g][mt][r] = fmaf(sc, blk[g][mt][r], acc[g][mt][r]);
+        }
+      }
+    }  // kbi
+    __syncthreads();
+  }
+  if constexpr (DUMP) return;
+
+  // ---- wave partials -> LDS (over the q stage), summed in wave order ----
+  float* red = reinterpret_cast<float*>(&qsm[0][0]);  // [4][G][16][BM]
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) red[((w * G + g) * 16 + li) * BM + 16 * mt + 4 * t + r] = acc[g][mt][r];
+  __syncthreads();
+  for (int idx = tid; idx < 16 * BM; idx += 256) {
+    const int rr = idx & 15, mm = idx >> 4;
+    const int n = n0 + rr, m = mb + mm;
+    if (m >= a.nb || n >= N) continue;
+    float v[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float sacc = red[((0 * G + g) * 16 + rr) * BM + mm];
+#pragma unroll
+      for (int ww = 1; ww < 4; ++ww) sacc = sacc + red[((ww * G + g) * 16 + rr) * BM + mm];
+      v[g] = sacc;
+    }
+    float* o = &y[(size_t)(a.m0 + m) * ldy + n];
+    if constexpr (MODE == BTF_GEMV_SWIGLU)
+      *o = v[0] / (1.0f + expf(-v[0])) * v[G - 1];
+    else if constexpr (MODE == BTF_GEMV_ADD)
+      *o += v[0];
+    else
+      *o = v[0];
+  }
+}
+
+template <int MT, bool DUMP>
+void by_mode_ks(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int KB = MT >= 2 ? 1 : 2;  // small stages: occupancy (4-5 waves per SIMD) beats bytes per round
+  if (mode == BTF_GEMV_STORE)
+    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
+  else if (mode == BTF_GEMV_ADD)
+    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
+}
+
 template <int MT, bool DUMP>
 void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int KB = MT >= 4 ? 1 : 8;
@@ -249,7 +560,9 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
               hipStream_t st, const DevState& ds) {
   (void)ds;
   MfmaArgs a{};
-  const int rows_real = mode == BTF_GEMV_SWIGLU ? 32 : 64;
+  // up to 32 activation rows: the K-split 16-row tile; more: the 64-row tile
+  const bool ks = nb <= 32;
+  const int rows_real = ks ? 16 : mode == BTF_GEMV_SWIGLU ? 32 : 64;
   const int nuse = mode == BTF_GEMV_SWIGLU ? 1 : nseg;
   int tiles = 0;
   for (int i = 0; i < 3; ++i) {
@@ -282,6 +595,13 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   const int BM = 16 * MT;
   const dim3 grid(tiles, (nb + BM - 1) / BM);
   const bool dmp = dump != nullptr;
+  if (ks) {
+    if (MT == 1)
+      dmp ? by_mode_ks<1, true>(mode, a, grid, st) : by_mode_ks<1, false>(mode, a, grid, st);
+    else
+      dmp ? by_mode_ks<2, true>(mode, a, grid, st) : by_mode_ks<2, false>(mode, a, grid, st);
+    return launch_status("gemm_ks_kernel");
+  }
   if (MT == 1)
     dmp ? by_mode<1, true>(mode, a, grid, st) : by_mode<1, false>(mode, a, grid, st);
   else if (MT == 2)

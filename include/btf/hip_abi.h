@@ -161,7 +161,7 @@ int btf_hip_launch_gemv_ptq1_0(const btf_gemv_seg* segs, int nseg, int K, int M,
                                btf_stream_t stream);
 
 /* GEMV path policy: batches of M >= mfma_min_m rows run on the int8-MFMA
- * kernel, smaller ones on the v_dot4 kernel (default 5; K > 32768 always
+ * kernels, smaller ones on the v_dot4 kernel (default 3; K > 32768 always
  * takes the MFMA kernel). 0 restores the default.
  * Process-global; for tests and benchmarks. Returns the previous value. */
 int btf_hip_gemv_set_policy(int mfma_min_m);

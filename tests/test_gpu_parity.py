@@ -295,6 +295,44 @@ def test_gemm_batched_and_prefill(hip, oracle, M):
     assert_close_1e3(host(y), ref, f"M={M}")
 
 
+@pytest.mark.parametrize("K,M", [(128, 3), (384, 17), (1152, 5), (3200, 32), (17536, 9)])
+def test_gemm_k_split_tile_edges(hip, oracle, K, M):
+    """Batches of 3..32 rows run on the K-split 16-row tile (each wave a
+    quarter of the 128-column blocks): block counts that do not split evenly
+    (1 block: three waves idle; 3, 9, 25, 137 blocks), one and two 16-row
+    activation tiles with dead rows, 16-row weight tiles with dead rows
+    (N = 37, 9), and the three modes, against the emulator GEMV."""
+    rng = np.random.default_rng(K + 1000 * M)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    act = q8_dev(q, d, s, hip)
+    torch = _torch()
+    G = hip.GemvMode
+    Ns = [37, 9]
+    mats = [random_mat(oracle, rng, n, K) for n in Ns]
+    ys = [zeros((M, n + 1), torch.float32) for n in Ns]
+    segs = [hip.GemvSeg(dev(c), dev(sc), n, y, n + 1) for (c, sc), n, y in zip(mats, Ns, ys)]
+    hip.launch_gemv(segs, K, M, act, G.kStore, stream())
+    for (c, sc), n, y in zip(mats, Ns, ys):
+        got = host(y)
+        assert_close_1e3(got[:, :n], oracle.gemv(c, sc, K, q, d, s), f"store K={K} M={M} N={n}")
+        assert np.all(got[:, n:] == 0), "wrote past N"
+    y0 = rng.standard_normal((M, Ns[0])).astype(np.float32)
+    yd = dev(y0)
+    hip.launch_gemv([hip.GemvSeg(dev(mats[0][0]), dev(mats[0][1]), Ns[0], yd, Ns[0])], K, M, act, G.kAdd,
+                    stream())
+    assert_close_1e3(host(yd), oracle.gemv(mats[0][0], mats[0][1], K, q, d, s, y=y0.copy(), add=True), "add")
+    up = random_mat(oracle, rng, Ns[0], K)
+    g = zeros((M, Ns[0]), torch.float32)
+    hip.launch_gemv([hip.GemvSeg(dev(mats[0][0]), dev(mats[0][1]), Ns[0], g, Ns[0]),
+                     hip.GemvSeg(dev(up[0]), dev(up[1]), Ns[0], None, 0)], K, M, act, G.kSwiglu, stream())
+    ref = oracle.swiglu(oracle.gemv(mats[0][0], mats[0][1], K, q, d, s), oracle.gemv(up[0], up[1], K, q, d, s))
+    assert_close_1e3(host(g), ref, "swiglu")
+    I_ref = oracle.gemv_i32(mats[1][0], K, q, s)
+    out = zeros((M, Ns[1], K // 32), torch.int32)
+    hip.gemv_i32_dump(dev(mats[1][0]), Ns[1], K, M, act, out, stream())
+    assert np.array_equal(host(out), I_ref)
+
+
 def test_prep_then_gemv_end_to_end(hip, oracle):
     """GPU quantize feeding the GPU GEMV equals oracle quantize + emulator GEMV."""
     rng = np.random.default_rng(99)
