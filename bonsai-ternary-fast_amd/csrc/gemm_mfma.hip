@@ -541,6 +541,246 @@ void by_mode_ks(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
 }
 
+// Prefill tile (more than 32 activation rows): a workgroup owns 64 staged
+// weight rows (swiglu: 32 gate rows and the same 32 up rows) and BM = 32 * MW
+// activation rows; wave (wn, wm) = (w & 1, w >> 1) computes 32 staged rows x
+// 16 * MW activation rows, 2 x MW MFMA tiles per 32-column sub-block from 2 B
+// and MW A fragments (swiglu: its two B tiles are the gate and up rows of the same
+// 16 outputs, so the epilogue stays in the lane). Per output the sums follow
+// the 64-row kernel's order: blk = d * I over the block's sub-blocks, then
+// acc += scale * blk per block.
+template <int MW, int KB, int MODE>
+__global__ void __launch_bounds__(256) gemm_pf_kernel(MfmaArgs a) {
+  constexpr int BM = 32 * MW;
+  constexpr int CS = 8 * KB + 1;
+  constexpr int QS = 32 * KB + 2;
+  constexpr int NCV = (64 * 2 * KB + 255) / 256;
+  constexpr int NSV = (64 * KB + 255) / 256;
+  constexpr int NQV = (BM * 8 * KB + 255) / 256;
+  constexpr int NDV = (BM * 4 * KB + 255) / 256;
+  constexpr bool SW = MODE == BTF_GEMV_SWIGLU;
+  __shared__ uint32_t cs[64 * CS];
+  __shared__ uint16_t scs[64 * KB];
+  __shared__ uint32_t qsm[BM * QS];
+  __shared__ float dsm[4 * KB][BM];
+  __shared__ int32_t nsm[4 * KB][BM];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int wn = w & 1, wm = w >> 1;
+  const int li = lane & 15;
+  const int t = lane >> 4;
+
+  const int bx = blockIdx.x;
+  const int seg = (bx >= a.tile_start[1]) + (bx >= a.tile_start[2]);
+  const uint8_t* codes = seg == 0 ? a.codes[0] : seg == 1 ? a.codes[1] : a.codes[2];
+  const uint16_t* scales = seg == 0 ? a.scales[0] : seg == 1 ? a.scales[1] : a.scales[2];
+  float* y = seg == 0 ? a.y[0] : seg == 1 ? a.y[1] : a.y[2];
+  const int N = seg == 0 ? a.N[0] : seg == 1 ? a.N[1] : a.N[2];
+  const int ldy = seg == 0 ? a.ldy[0] : seg == 1 ? a.ldy[1] : a.ldy[2];
+  const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
+  const int K = a.K;
+  const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
+  constexpr int ROWS_REAL = SW ? 32 : 64;
+  const int n0 = (bx - tile0) * ROWS_REAL;
+  const int mb = blockIdx.y * BM;
+
+  // staged row of this wave's B tile j (lane row li added at use)
+  int srow[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) srow[j] = SW ? 32 * j + 16 * wn : 32 * wn + 16 * j;
+
+  float acc[2][MW][4], blk[2][MW][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[j][mt][r] = 0.f;
+
+  u32x4 rc[NCV], rq[NQV];
+  uint16_t rsc[NSV];
+  float rd[NDV];
+  int rs[NDV];
+  auto fetch = [&](int kb0) {
+    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (2 * KB), part = i - r * (2 * KB);
+      rc[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < 64 * 2 * KB && part < 2 * nkb) {
+        const bool up = SW && r >= 32;
+        const int nr = n0 + (SW ? (r & 31) : r);
+        const int nc = nr < N ? nr : N - 1;
+        const uint8_t* cb = up ? a.up_codes : codes;
+        rc[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / KB, jj = i - r * KB;
+      rsc[j] = 0;
+      if (i < 64 * KB && jj < nkb) {
+        const bool up = SW && r >= 32;
+        const int nr = n0 + (SW ? (r & 31) : r);
+        const int nc = nr < N ? nr : N - 1;
+        const uint16_t* sb = up ? a.up_scales : scales;
+        rsc[j] = sb[(size_t)nc * nsc + kb0 + jj];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (8 * KB), part = i - r * (8 * KB);
+      const int m = mb + r;
+      rq[j] = u32x4{0u, 0u, 0u, 0u};
+      if (i < BM * 8 * KB && part < 8 * nkb && m < a.nb)
+        rq[j] = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i / (4 * KB), sb = i - r * (4 * KB);
+      const int m = mb + r;
+      rd[j] = 0.f;
+      rs[j] = 0;
+      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) {
+        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
+        rd[j] = a.d[o];
+        rs[j] = a.s[o];
+      }
+    }
+  };
+  auto stage = [&]() {
+#pragma unroll
+    for (int j = 0; j < NCV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < 64 * 2 * KB) {
+        const int r = i / (2 * KB), part = i - r * (2 * KB);
+        uint32_t* o = &cs[r * CS + 4 * part];
+        o[0] = rc[j].x; o[1] = rc[j].y; o[2] = rc[j].z; o[3] = rc[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NSV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < 64 * KB) scs[i] = rsc[j];
+    }
+#pragma unroll
+    for (int j = 0; j < NQV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < BM * 8 * KB) {
+        const int r = i / (8 * KB), part = i - r * (8 * KB);
+        uint32_t* o = &qsm[r * QS + 4 * part];
+        o[0] = rq[j].x; o[1] = rq[j].y; o[2] = rq[j].z; o[3] = rq[j].w;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < NDV; ++j) {
+      const int i = tid + 256 * j;
+      if (i < BM * 4 * KB) {
+        const int r = i / (4 * KB), sb = i - r * (4 * KB);
+        dsm[sb][r] = rd[j];
+        nsm[sb][r] = -rs[j];
+      }
+    }
+  };
+
+  fetch(0);
+  for (int kb0 = 0; kb0 < nsc; kb0 += KB) {
+    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;
+    stage();
+    __syncthreads();
+    if (kb0 + KB < nsc) fetch(kb0 + KB);  // in flight while this stage is dotted
+
+    for (int kbi = 0; kbi < nkb; ++kbi) {
+#pragma unroll
+      for (int sb = 0; sb < 4; ++sb) {
+        const int sbx = 4 * kbi + sb;
+        long bfrag[2];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const uint32_t word = cs[(srow[j] + li) * CS + 2 * sbx + (t >> 1)];
+          const int sh = 4 * (t & 1);
+          const uint32_t lo = (word >> sh) & 0x03030303u;
+          const uint32_t hi = (word >> (sh + 2)) & 0x03030303u;
+          bfrag[j] = (long)(((uint64_t)hi << 32) | lo);
+        }
+#pragma unroll
+        for (int mt = 0; mt < MW; ++mt) {
+          const int mr = 16 * MW * wm + 16 * mt;
+          const uint32_t* ap = &qsm[(mr + li) * QS + 8 * sbx + 2 * t];
+          const long afrag = (long)(((uint64_t)ap[1] << 32) | ap[0]);
+          v4i cin;
+          float dv[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            cin[r] = nsm[sbx][mr + 4 * t + r];
+            dv[r] = dsm[sbx][mr + 4 * t + r];
+          }
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], cin, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              blk[j][mt][r] = sb == 0 ? dv[r] * (float)I[r] : fmaf(dv[r], (float)I[r], blk[j][mt][r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float sc = h2f(scs[(srow[j] + li) * KB + kbi]);
+#pragma unroll
+        for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) acc[j][mt][r] = fmaf(sc, blk[j][mt][r], acc[j][mt][r]);
+      }
+    }
+    __syncthreads();
+  }
+
+#pragma unroll
+  for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mb + 16 * MW * wm + 16 * mt + 4 * t + r;
+      if (m >= a.nb) continue;
+      if constexpr (SW) {
+        const int n = n0 + 16 * wn + li;
+        if (n < N) {
+          const float g = acc[0][mt][r], u = acc[1][mt][r];
+          y[(size_t)(a.m0 + m) * ldy + n] = g / (1.0f + expf(-g)) * u;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + srow[j] + li;
+          if (n < N) {
+            float* o = &y[(size_t)(a.m0 + m) * ldy + n];
+            if constexpr (MODE == BTF_GEMV_ADD)
+              *o += acc[j][mt][r];
+            else
+              *o = acc[j][mt][r];
+          }
+        }
+      }
+    }
+}
+
+template <int MW>
+void by_mode_pf(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int KB = 1;
+  if (mode == BTF_GEMV_STORE)
+    hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_STORE>), grid, dim3(256), 0, st, a);
+  else if (mode == BTF_GEMV_ADD)
+    hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_ADD>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_SWIGLU>), grid, dim3(256), 0, st, a);
+}
+
 template <int MT, bool DUMP>
 void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int KB = MT >= 4 ? 1 : 8;
@@ -558,7 +798,6 @@ int mfma_rows_per_pass() { return 64; }
 
 int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& act, int mode, int32_t* dump,
               hipStream_t st, const DevState& ds) {
-  (void)ds;
   MfmaArgs a{};
   // up to 32 activation rows: the K-split 16-row tile; more: the 64-row tile
   const bool ks = nb <= 32;
@@ -601,6 +840,15 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
     else
       dmp ? by_mode_ks<2, true>(mode, a, grid, st) : by_mode_ks<2, false>(mode, a, grid, st);
     return launch_status("gemm_ks_kernel");
+  }
+  if (!dmp && nb > 32) {
+    // 128 activation rows per tile while that still gives two workgroups per CU, else 64
+    const int cus = ds.cu_count > 0 ? ds.cu_count : 256;
+    if ((int64_t)tiles * ((nb + 127) / 128) >= 2 * cus)
+      by_mode_pf<4>(mode, a, dim3(tiles, (nb + 127) / 128), st);
+    else
+      by_mode_pf<2>(mode, a, dim3(tiles, (nb + 63) / 64), st);
+    return launch_status("gemm_pf_kernel");
   }
   if (MT == 1)
     dmp ? by_mode<1, true>(mode, a, grid, st) : by_mode<1, false>(mode, a, grid, st);

@@ -333,6 +333,65 @@ def test_gemm_k_split_tile_edges(hip, oracle, K, M):
     assert np.array_equal(host(out), I_ref)
 
 
+@pytest.mark.parametrize("K,M", [(1024, 33), (5120, 200), (2048, 512)])
+def test_gemm_prefill_tile_modes(hip, oracle, K, M):
+    """More than 32 rows run on the prefill tile (64 staged weight rows x 128
+    activation rows, 2 x 4 MFMA tiles per wave): three store segments with
+    dead weight rows (N = 37, 70, 9), a dead activation tail (M = 33, 200),
+    add, and swiglu (gate and up of the same outputs in one wave), against
+    the emulator GEMV."""
+    rng = np.random.default_rng(K + M)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    act = q8_dev(q, d, s, hip)
+    torch = _torch()
+    G = hip.GemvMode
+    Ns = [37, 70, 9]
+    mats = [random_mat(oracle, rng, n, K) for n in Ns]
+    ys = [zeros((M, n + 3), torch.float32) for n in Ns]
+    segs = [hip.GemvSeg(dev(c), dev(sc), n, y, n + 3) for (c, sc), n, y in zip(mats, Ns, ys)]
+    hip.launch_gemv(segs, K, M, act, G.kStore, stream())
+    for (c, sc), n, y in zip(mats, Ns, ys):
+        got = host(y)
+        assert_close_1e3(got[:, :n], oracle.gemv(c, sc, K, q, d, s), f"store K={K} M={M} N={n}")
+        assert np.all(got[:, n:] == 0), "wrote past N"
+    y0 = rng.standard_normal((M, Ns[1])).astype(np.float32)
+    yd = dev(y0)
+    hip.launch_gemv([hip.GemvSeg(dev(mats[1][0]), dev(mats[1][1]), Ns[1], yd, Ns[1])], K, M, act, G.kAdd,
+                    stream())
+    assert_close_1e3(host(yd), oracle.gemv(mats[1][0], mats[1][1], K, q, d, s, y=y0.copy(), add=True), "add")
+    up = random_mat(oracle, rng, Ns[1], K)
+    g = zeros((M, Ns[1]), torch.float32)
+    hip.launch_gemv([hip.GemvSeg(dev(mats[1][0]), dev(mats[1][1]), Ns[1], g, Ns[1]),
+                     hip.GemvSeg(dev(up[0]), dev(up[1]), Ns[1], None, 0)], K, M, act, G.kSwiglu, stream())
+    ref = oracle.swiglu(oracle.gemv(mats[1][0], mats[1][1], K, q, d, s), oracle.gemv(up[0], up[1], K, q, d, s))
+    assert_close_1e3(host(g), ref, "swiglu")
+
+
+def test_gemm_prefill_wide_tile(hip, oracle):
+    """Grids of at least two workgroups per CU take the 128-row activation
+    tile: M = 400 (a dead tail of 112 rows in the last tile), store on
+    N = 16421 and swiglu on N = 8197, checked on sampled output columns (the
+    first, a middle and the last weight tiles) against the emulator GEMV."""
+    K, M = 1024, 400
+    rng = np.random.default_rng(400)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    act = q8_dev(q, d, s, hip)
+    torch = _torch()
+    G = hip.GemvMode
+    for mode, N in ((G.kStore, 16421), (G.kSwiglu, 8197)):
+        sel = np.r_[0:70, N // 2 - 40:N // 2 + 40, N - 37:N]
+        mats = [random_mat(oracle, rng, N, K) for _ in range(2 if mode == G.kSwiglu else 1)]
+        y = zeros((M, N), torch.float32)
+        segs = [hip.GemvSeg(dev(mats[0][0]), dev(mats[0][1]), N, y, N)]
+        if mode == G.kSwiglu:
+            segs.append(hip.GemvSeg(dev(mats[1][0]), dev(mats[1][1]), N, None, 0))
+        hip.launch_gemv(segs, K, M, act, mode, stream())
+        refs = [oracle.gemv(np.ascontiguousarray(c[sel]), np.ascontiguousarray(sc[sel]), K, q, d, s)
+                for c, sc in mats]
+        ref = oracle.swiglu(*refs) if mode == G.kSwiglu else refs[0]
+        assert_close_1e3(host(y)[:, sel], ref, f"mode={mode} N={N}")
+
+
 def test_prep_then_gemv_end_to_end(hip, oracle):
     """GPU quantize feeding the GPU GEMV equals oracle quantize + emulator GEMV."""
     rng = np.random.default_rng(99)
