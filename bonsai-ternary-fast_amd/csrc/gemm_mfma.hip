@@ -286,16 +286,16 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
   }
 }
 
-// K-split tile for batched decode (up to 32 activation rows): a workgroup
-// owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows) and BM
-// activation rows, and wave w walks its quarter of the 128-column blocks,
+// K-split tile for batched decode (up to 32 activation rows): a workgroup of
+// NW waves owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows)
+// and BM activation rows, and wave w walks its 1/NW of the 128-column blocks,
 // staging its own codes, scales, q and d / -s in a private LDS region. Four
-// times as many workgroups as the 64-row tile and a quarter of the serial
-// MFMA chain per wave; the activation is re-read from L2 by each tile. Per
-// wave the row sums follow the 64-row kernel's order over its blocks, and the
-// four wave partials are added in wave order: ((p0 + p1) + p2) + p3.
-template <int MT, int KB, int MODE, bool DUMP>
-__global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
+// times as many workgroups as the 64-row tile and 1/NW of the serial MFMA
+// chain per wave; the activation is re-read from L2 by each tile. Per wave
+// the row sums follow the 64-row kernel's order over its blocks, and the NW
+// wave partials are added in wave order: ((p0 + p1) + p2) + ...
+template <int NW, int MT, int KB, int MODE, bool DUMP>
+__global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   constexpr int BM = 16 * MT;
   constexpr int G = MODE == BTF_GEMV_SWIGLU ? 2 : 1;  // 16-row groups: gate (and up)
   constexpr int RW = 16 * G;                          // staged rows per wave
@@ -305,12 +305,12 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
   constexpr int NSV = (RW * KB + 63) / 64;      // scale loads
   constexpr int NQV = (BM * 8 * KB + 63) / 64;  // 16-byte q loads
   constexpr int NDV = (BM * 4 * KB + 63) / 64;  // d / s loads
-  __shared__ uint32_t cs[4][RW * CS];
-  __shared__ uint16_t scs[4][RW * KB];
-  __shared__ uint32_t qsm[4][BM * QS];
-  __shared__ float dsm[4][4 * KB][BM];
-  __shared__ int32_t nsm[4][4 * KB][BM];
-  static_assert(sizeof(qsm) >= 4 * G * 16 * BM * sizeof(float), "partials alias the q stage");
+  __shared__ uint32_t cs[NW][RW * CS];
+  __shared__ uint16_t scs[NW][RW * KB];
+  __shared__ uint32_t qsm[NW][BM * QS];
+  __shared__ float dsm[NW][4 * KB][BM];
+  __shared__ int32_t nsm[NW][4 * KB][BM];
+  static_assert(sizeof(qsm) >= NW * G * 16 * BM * sizeof(float), "partials alias the q stage");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -333,8 +333,8 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
 
   // this wave's blocks [kw0, kw1); every wave runs niter iterations so the
   // workgroup barriers match
-  const int kw0 = nsc * w / 4, kw1 = nsc * (w + 1) / 4;
-  const int niter = ((nsc + 3) / 4 + KB - 1) / KB;
+  const int kw0 = nsc * w / NW, kw1 = nsc * (w + 1) / NW;
+  const int niter = ((nsc + NW - 1) / NW + KB - 1) / KB;
 
   float acc[G][MT][4], blk[G][MT][4];
 #pragma unroll
@@ -500,7 +500,7 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
   if constexpr (DUMP) return;
 
   // ---- wave partials -> LDS (over the q stage), summed in wave order ----
-  float* red = reinterpret_cast<float*>(&qsm[0][0]);  // [4][G][16][BM]
+  float* red = reinterpret_cast<float*>(&qsm[0][0]);  // [NW][G][16][BM]
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -508,7 +508,7 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[((w * G + g) * 16 + li) * BM + 16 * mt + 4 * t + r] = acc[g][mt][r];
   __syncthreads();
-  for (int idx = tid; idx < 16 * BM; idx += 256) {
+  for (int idx = tid; idx < 16 * BM; idx += 64 * NW) {
     const int rr = idx & 15, mm = idx >> 4;
     const int n = n0 + rr, m = mb + mm;
     if (m >= a.nb || n >= N) continue;
@@ -517,7 +517,7 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
     for (int g = 0; g < G; ++g) {
       float sacc = red[((0 * G + g) * 16 + rr) * BM + mm];
 #pragma unroll
-      for (int ww = 1; ww < 4; ++ww) sacc = sacc + red[((ww * G + g) * 16 + rr) * BM + mm];
+      for (int ww = 1; ww < NW; ++ww) sacc = sacc + red[((ww * G + g) * 16 + rr) * BM + mm];
       v[g] = sacc;
     }
     float* o = &y[(size_t)(a.m0 + m) * ldy + n];
@@ -530,15 +530,23 @@ __global__ void __launch_bounds__(256) gemm_ks_kernel(MfmaArgs a) {
   }
 }
 
-template <int MT, bool DUMP>
+template <int NW, int MT, bool DUMP>
 void by_mode_ks(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int KB = MT >= 2 ? 1 : 2;  // small stages: occupancy (4-5 waves per SIMD) beats bytes per round
   if (mode == BTF_GEMV_STORE)
-    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(64 * NW), 0, st, a);
   else if (mode == BTF_GEMV_ADD)
-    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(64 * NW), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_ks_kernel<MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(64 * NW), 0, st, a);
+}
+
+template <int MT, bool DUMP>
+void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  if (nw == 8)
+    by_mode_ks<8, MT, DUMP>(mode, a, grid, st);
+  else
+    by_mode_ks<4, MT, DUMP>(mode, a, grid, st);
 }
 
 // Prefill tile (more than 32 activation rows): a workgroup owns 64 staged
@@ -835,10 +843,14 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   const dim3 grid(tiles, (nb + BM - 1) / BM);
   const bool dmp = dump != nullptr;
   if (ks) {
+    // 8 waves split K for one activation tile (measured: down 29.6 -> 25.2 us and
+    // QKV 11.0 -> 10.1 us at M = 8), except gate+up at K = 5120 (27 -> 31 us);
+    // with two activation tiles 8 waves were slower on every shape
+    const int nw = MT == 1 && (K >= 8192 || mode != BTF_GEMV_SWIGLU) ? 8 : 4;
     if (MT == 1)
-      dmp ? by_mode_ks<1, true>(mode, a, grid, st) : by_mode_ks<1, false>(mode, a, grid, st);
+      dmp ? by_waves_ks<1, true>(nw, mode, a, grid, st) : by_waves_ks<1, false>(nw, mode, a, grid, st);
     else
-      dmp ? by_mode_ks<2, true>(mode, a, grid, st) : by_mode_ks<2, false>(mode, a, grid, st);
+      dmp ? by_waves_ks<2, true>(nw, mode, a, grid, st) : by_waves_ks<2, false>(nw, mode, a, grid, st);
     return launch_status("gemm_ks_kernel");
   }
   if (!dmp && nb > 32) {
