@@ -831,7 +831,7 @@ def main():
             tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
             roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
                     "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                    "kernel": f"{dom} GEMM (gemm_pf_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
+                    "kernel": f"{dom} GEMM (gemm_pf2_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
 
     out = {
         "metric": METRIC,

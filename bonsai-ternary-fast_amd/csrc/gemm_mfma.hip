@@ -789,6 +789,224 @@ void by_mode_pf(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_SWIGLU>), grid, dim3(256), 0, st, a);
 }
 
+// ---- LDS-direct prefill tile ----
+// vmcnt(N) alone (expcnt, lgkmcnt not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+// One wave-wide load into LDS: lane l's 16 bytes from g land at LDS byte
+// address lds + 16 l; a 2-byte load fills the low half of the 4-byte slot at
+// lds + 4 l (sub-dword loads keep 4-byte lane slots). Issued as inline assembly so that the compiler's
+// wait insertion does not order every later LDS read behind it; the kernel
+// waits with wait_vm itself. M0 (the LDS base) is set in the same statement,
+// with the one wait state an LDS-direct load needs after an SALU write of M0;
+// the compiler reserves M0 and no other code of the kernel reads it (checked
+// in its assembly: every M0 write is one of these).
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ushort %0, off" : : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+
+// The prefill tile of gemm_pf_kernel (64 staged weight rows x BM = 32 * MW
+// activation rows, wave (w & 1, w >> 1) computes 32 x 16 * MW) fed by an
+// S-stage ring of LDS-direct loads: after the barrier of block k each wave
+// issues its share of block k + S - 1, so a load has S - 1 blocks of compute
+// to arrive in and no staging registers. The 2-bit codes are mapped to int8
+// {-1, 0, +1} with one byte permute per word, so the MFMA yields
+// I = sum q * w directly (accumulator 0) and s is not read. Stage layout:
+// q [BM][128 B] with the 16-byte chunk c of row r at slot c ^ (r & 7) (the A
+// fragments of 16 rows fall in 8 bank groups), codes [64][32 B], d [BM][4],
+// scales [64] in 4-byte slots. Same sums, in the same order, as gemm_pf_kernel.
+template <int MW, int S, int MODE>
+__global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
+  constexpr int BM = 32 * MW;
+  constexpr bool SW = MODE == BTF_GEMV_SWIGLU;
+  constexpr int QB = BM * 128, CB = 64 * 32, DB = BM * 16, SCB = 64 * 4;
+  constexpr int STG = QB + CB + DB + SCB;
+  constexpr int NQ = BM / 32;  // q loads per wave per block
+  static_assert(STG % 16 == 0, "stage alignment");
+  __shared__ __attribute__((aligned(16))) uint8_t ring[S * STG];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: LDS bases and roles
+  const int wn = w & 1, wm = w >> 1;
+  const int li = lane & 15;
+  const int t = lane >> 4;
+
+  const int bx = blockIdx.x;
+  const int seg = (bx >= a.tile_start[1]) + (bx >= a.tile_start[2]);
+  const uint8_t* codes = seg == 0 ? a.codes[0] : seg == 1 ? a.codes[1] : a.codes[2];
+  const uint16_t* scales = seg == 0 ? a.scales[0] : seg == 1 ? a.scales[1] : a.scales[2];
+  float* y = seg == 0 ? a.y[0] : seg == 1 ? a.y[1] : a.y[2];
+  const int N = seg == 0 ? a.N[0] : seg == 1 ? a.N[1] : a.N[2];
+  const int ldy = seg == 0 ? a.ldy[0] : seg == 1 ? a.ldy[1] : a.ldy[2];
+  const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
+  const int K = a.K;
+  const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
+  constexpr int ROWS_REAL = SW ? 32 : 64;
+  const int n0 = (bx - tile0) * ROWS_REAL;
+  const int mb = blockIdx.y * BM;
+  const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)ring;  // LDS byte address
+
+  // ---- this lane's load sources (block 0; block kb adds kb * step) ----
+  // q: load i covers slots (w * NQ + i) * 64 + lane -> row P / 8, slot P % 8
+  const int8_t* qsrc[NQ];
+#pragma unroll
+  for (int i = 0; i < NQ; ++i) {
+    const int P = (w * NQ + i) * 64 + lane;
+    const int r = P >> 3, c = (P & 7) ^ (r & 7);
+    const int m = mb + r < a.nb ? mb + r : a.nb - 1;
+    qsrc[i] = a.q + (size_t)(a.m0 + m) * K + 16 * c;
+  }
+  // codes (waves 0, 1): slot P = w * 64 + lane -> staged row P / 2, half P % 2
+  const uint8_t* csrc;
+  {
+    const int P = (w & 1) * 64 + lane;
+    const int r = P >> 1;
+    const int nr = n0 + (SW ? (r & 31) : r);
+    const int nc = nr < N ? nr : N - 1;
+    csrc = (SW && r >= 32 ? a.up_codes : codes) + (size_t)nc * rowb + 16 * (P & 1);
+  }
+  // d (waves 2, 3): row (w - 2) * 64 + lane; scales (wave 3): staged row lane
+  const float* dsrc;
+  {
+    const int r = ((w - 2) & 1) * 64 + lane;
+    const int m = mb + r < a.nb ? mb + r : a.nb - 1;
+    dsrc = a.d + (size_t)(a.m0 + m) * nsub;
+  }
+  const uint16_t* ssrc;
+  {
+    const int nr = n0 + (SW ? (lane & 31) : lane);
+    const int nc = nr < N ? nr : N - 1;
+    ssrc = (SW && lane >= 32 ? a.up_scales : scales) + (size_t)nc * nsc;
+  }
+  // Loads per wave per block: NQ q + (waves 0, 1: codes; waves 2, 3: d when
+  // BM covers them) + (wave 3: scales).
+  const bool do_d = w >= 2 && (w - 2) * 64 < BM;
+  auto issue = [&](int kb) {
+    const int kc = kb < nsc ? kb : nsc - 1;  // blocks past the end reload the last (never read)
+    const uint32_t st = ring0 + (uint32_t)((kb % S) * STG);
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) lds_dma16(qsrc[i] + (size_t)kc * 128, st + (uint32_t)((w * NQ + i) * 1024));
+    if (w < 2) lds_dma16(csrc + (size_t)kc * 32, st + QB + (uint32_t)(w * 1024));
+    if (do_d) lds_dma16(dsrc + (size_t)kc * 4, st + QB + CB + (uint32_t)((w - 2) * 1024));
+    if (w == 3) lds_dma2(ssrc + kc, st + QB + CB + DB);
+  };
+
+  int srow[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) srow[j] = SW ? 32 * j + 16 * wn : 32 * wn + 16 * j;
+
+  float acc[2][MW][4], blk[2][MW][4];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[j][mt][r] = 0.f;
+
+#pragma unroll
+  for (int kb = 0; kb < S - 1; ++kb) issue(kb);
+  const v4i zero = {0, 0, 0, 0};
+  for (int kb = 0; kb < nsc; ++kb) {
+    // this wave's loads of block kb have landed once at most (S - 2) blocks of
+    // its loads are outstanding
+    constexpr int L012 = NQ + 1, L3 = NQ + (BM > 64 ? 1 : 0) + 1;
+    if (w == 3)
+      wait_vm<L3 * (S - 2)>();
+    else
+      wait_vm<L012 * (S - 2)>();
+    __syncthreads();  // every wave's loads of kb landed; every wave is done with block kb - 1
+    issue(kb + S - 1);  // into the stage of block kb - 1
+    const uint8_t* stg = ring + (kb % S) * STG;
+    const uint8_t* cst = stg + QB;
+    const float* dst = reinterpret_cast<const float*>(stg + QB + CB);
+    const uint8_t* sst = stg + QB + CB + DB;
+#pragma unroll
+    for (int sb = 0; sb < 4; ++sb) {
+      long bfrag[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const uint32_t word = *reinterpret_cast<const uint32_t*>(cst + (srow[j] + li) * 32 + 4 * (2 * sb + (t >> 1)));
+        const int sh = 4 * (t & 1);
+        const uint32_t lo = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> sh) & 0x03030303u);
+        const uint32_t hi = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> (sh + 2)) & 0x03030303u);
+        bfrag[j] = (long)(((uint64_t)hi << 32) | lo);
+      }
+#pragma unroll
+      for (int mt = 0; mt < MW; ++mt) {
+        const int mr = 16 * MW * wm + 16 * mt;
+        const int r = mr + li;
+        const long afrag = *reinterpret_cast<const long*>(stg + r * 128 + 16 * ((2 * sb + (t >> 1)) ^ (r & 7)) +
+                                                          8 * (t & 1));
+        float dv[4];
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) dv[rr] = dst[(mr + 4 * t + rr) * 4 + sb];
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], zero, 0, 0, 0);
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr)
+            blk[j][mt][rr] = sb == 0 ? dv[rr] * (float)I[rr] : fmaf(dv[rr], (float)I[rr], blk[j][mt][rr]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const float sc = h2f(*reinterpret_cast<const uint16_t*>(sst + 4 * (srow[j] + li)));
+#pragma unroll
+      for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[j][mt][r] = fmaf(sc, blk[j][mt][r], acc[j][mt][r]);
+    }
+  }
+  wait_vm<0>();  // the trailing loads land before the workgroup's LDS is released
+
+#pragma unroll
+  for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = mb + 16 * MW * wm + 16 * mt + 4 * t + r;
+      if (m >= a.nb) continue;
+      if constexpr (SW) {
+        const int n = n0 + 16 * wn + li;
+        if (n < N) {
+          const float g = acc[0][mt][r], u = acc[1][mt][r];
+          y[(size_t)(a.m0 + m) * ldy + n] = g / (1.0f + expf(-g)) * u;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int n = n0 + srow[j] + li;
+          if (n < N) {
+            float* o = &y[(size_t)(a.m0 + m) * ldy + n];
+            if constexpr (MODE == BTF_GEMV_ADD)
+              *o += acc[j][mt][r];
+            else
+              *o = acc[j][mt][r];
+          }
+        }
+      }
+    }
+}
+
+template <int MW, int S>
+void by_mode_pf2(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  if (mode == BTF_GEMV_STORE)
+    hipLaunchKernelGGL((gemm_pf2_kernel<MW, S, BTF_GEMV_STORE>), grid, dim3(256), 0, st, a);
+  else if (mode == BTF_GEMV_ADD)
+    hipLaunchKernelGGL((gemm_pf2_kernel<MW, S, BTF_GEMV_ADD>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_pf2_kernel<MW, S, BTF_GEMV_SWIGLU>), grid, dim3(256), 0, st, a);
+}
+
 template <int MT, bool DUMP>
 void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int KB = MT >= 4 ? 1 : 8;
@@ -856,7 +1074,16 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   if (!dmp && nb > 32) {
     // 128 activation rows per tile while that still gives two workgroups per CU, else 64
     const int cus = ds.cu_count > 0 ? ds.cu_count : 256;
-    if ((int64_t)tiles * ((nb + 127) / 128) >= 2 * cus)
+    const bool wide = (int64_t)tiles * ((nb + 127) / 128) >= 2 * cus;
+    // the LDS-direct ring loads d in 16-byte pieces
+    if ((reinterpret_cast<uintptr_t>(act.d) & 15) == 0) {
+      if (wide)
+        by_mode_pf2<4, 2>(mode, a, dim3(tiles, (nb + 127) / 128), st);  // 41 KB: 3 workgroups per CU
+      else
+        by_mode_pf2<2, 3>(mode, a, dim3(tiles, (nb + 63) / 64), st);  // 34 KB: 4 workgroups per CU
+      return launch_status("gemm_pf2_kernel");
+    }
+    if (wide)
       by_mode_pf<4>(mode, a, dim3(tiles, (nb + 127) / 128), st);
     else
       by_mode_pf<2>(mode, a, dim3(tiles, (nb + 63) / 64), st);

@@ -392,6 +392,25 @@ def test_gemm_prefill_wide_tile(hip, oracle):
         assert_close_1e3(host(y)[:, sel], ref, f"mode={mode} N={N}")
 
 
+def test_gemm_prefill_unaligned_scales(hip, oracle):
+    """The prefill ring loads the activation scales d in 16-byte pieces; a d
+    array at an 8-byte (not 16-byte) aligned address takes the register-staged
+    prefill tile instead. Both against the emulator GEMV."""
+    K, M, N = 1024, 40, 45
+    rng = np.random.default_rng(41)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    codes, scales = random_mat(oracle, rng, N, K)
+    ref = oracle.gemv(codes, scales, K, q, d, s)
+    torch = _torch()
+    dbuf = zeros(d.size + 2, torch.float32)
+    dbuf[2:] = dev(d.reshape(-1))
+    for dptr in (dev(d), dbuf.data_ptr() + 8):
+        y = zeros((M, N), torch.float32)
+        act = hip.Q8Act(dev(q), dptr, dev(s))
+        hip.launch_gemv([hip.GemvSeg(dev(codes), dev(scales), N, y, N)], K, M, act, hip.GemvMode.kStore, stream())
+        assert_close_1e3(host(y), ref, "prefill d alignment")
+
+
 def test_prep_then_gemv_end_to_end(hip, oracle):
     """GPU quantize feeding the GPU GEMV equals oracle quantize + emulator GEMV."""
     rng = np.random.default_rng(99)
