@@ -289,8 +289,10 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
 // K-split tile for batched decode (up to 32 activation rows): a workgroup of
 // NW waves owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows)
 // and BM activation rows, and wave w walks its 1/NW of the 128-column blocks,
-// staging its own codes, scales, q and d / -s in a private LDS region. Four
-// times as many workgroups as the 64-row tile and 1/NW of the serial MFMA
+// staging its own codes, scales, q and d in a private LDS region (the codes
+// are permuted to int8 -1 / 0 / +1, so the MFMA yields I with accumulator 0
+// and s is not read). Four times as many workgroups as the 64-row tile and
+// 1/NW of the serial MFMA
 // chain per wave; the activation is re-read from L2 by each tile. Per wave
 // the row sums follow the 64-row kernel's order over its blocks, and the NW
 // wave partials are added in wave order: ((p0 + p1) + p2) + ...
@@ -309,7 +311,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   __shared__ uint16_t scs[NW][RW * KB];
   __shared__ uint32_t qsm[NW][BM * QS];
   __shared__ float dsm[NW][4 * KB][BM];
-  __shared__ int32_t nsm[NW][4 * KB][BM];
   static_assert(sizeof(qsm) >= NW * G * 16 * BM * sizeof(float), "partials alias the q stage");
 
   const int tid = threadIdx.x;
@@ -347,7 +348,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   u32x4 rc[NCV], rq[NQV];
   uint16_t rsc[NSV];
   float rd[NDV];
-  int rs[NDV];
   auto fetch = [&](int it) {
     const int kb0 = kw0 + it * KB;
     const int nkb = kw1 - kb0 < KB ? kw1 - kb0 : KB;  // may be <= 0 on the last iteration
@@ -390,12 +390,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
       const int r = i / (4 * KB), sb = i - r * (4 * KB);
       const int m = mb + r;
       rd[j] = 0.f;
-      rs[j] = 0;
-      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) {
-        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
-        rd[j] = a.d[o];
-        rs[j] = a.s[o];
-      }
+      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) rd[j] = a.d[(size_t)(a.m0 + m) * nsub + kb0 * 4 + sb];
     }
   };
   auto stage = [&]() {
@@ -428,7 +423,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
       if (i < BM * 4 * KB) {
         const int r = i / (4 * KB), sb = i - r * (4 * KB);
         dsm[w][sb][r] = rd[j];
-        nsm[w][sb][r] = -rs[j];
       }
     }
   };
@@ -451,19 +445,16 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
         for (int g = 0; g < G; ++g) {
           const uint32_t word = cs[w][(16 * g + li) * CS + 2 * sbx + (t >> 1)];
           const int sh = 4 * (t & 1);
-          const uint32_t lo = (word >> sh) & 0x03030303u;
-          const uint32_t hi = (word >> (sh + 2)) & 0x03030303u;
+          // codes 0 / 1 / 2 -> int8 -1 / 0 / +1: the MFMA gives I = sum q * w with accumulator 0
+          const uint32_t lo = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> sh) & 0x03030303u);
+          const uint32_t hi = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> (sh + 2)) & 0x03030303u);
           bfrag[g] = (long)(((uint64_t)hi << 32) | lo);
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
           const uint32_t* ap = &qsm[w][(16 * mt + li) * QS + 8 * sbx + 2 * t];
           const long afrag = (long)(((uint64_t)ap[1] << 32) | ap[0]);
-          v4i cin;
-          cin[0] = nsm[w][sbx][16 * mt + 4 * t + 0];
-          cin[1] = nsm[w][sbx][16 * mt + 4 * t + 1];
-          cin[2] = nsm[w][sbx][16 * mt + 4 * t + 2];
-          cin[3] = nsm[w][sbx][16 * mt + 4 * t + 3];
+          const v4i cin = {0, 0, 0, 0};
 #pragma unroll
           for (int g = 0; g < G; ++g) {
             const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[g], cin, 0, 0, 0);
