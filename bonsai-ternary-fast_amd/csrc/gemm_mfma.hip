@@ -1,13 +1,21 @@
 // gemm_mfma.hip -- ternary GEMM on T2 codes with int8 MFMA (gfx950), for
 // batched decode and prefill. Same contract as the reference's gemv_kernel
-// (src/cuda/kernels.cu:238-334) for M activation rows.
+// (src/cuda/kernels.cu:238-334) for M activation rows. Kernels:
+//   gemm_ks_kernel   up to 32 rows (batched decode): 16 weight rows per
+//                    workgroup, K split over its waves;
+//   gemm_pf2_kernel  more rows (prefill): 64 weight rows x 64 or 128
+//                    activation rows, fed by an LDS-direct ring;
+//   gemm_pf_kernel   the same tile staged through registers (activation
+//                    scales not 16-byte aligned);
+//   gemm_mfma_kernel the first 64-row tile, kept for the exact-I dump of more
+//                    than 32 rows.
 //
-// Tile: a workgroup of 4 waves owns 64 weight rows (wave w: rows 16w..16w+15;
-// swiglu: waves 0-1 gate rows, waves 2-3 the matching up rows) and
-// BM = 16*MT activation rows. The K loop walks 128-column blocks (one fp16
-// weight scale): codes (64 x 32 B), the block's scales, q (BM x 128 B) and the
-// activation d / -s (BM x 4) are staged in LDS, then every wave runs, per
-// 32-column sub-block,
+// The 64-row tile: a workgroup of 4 waves owns 64 weight rows (wave w: rows
+// 16w..16w+15; swiglu: waves 0-1 gate rows, waves 2-3 the matching up rows)
+// and BM = 16*MT activation rows. The K loop walks 128-column blocks (one
+// fp16 weight scale): codes (64 x 32 B), the block's scales, q (BM x 128 B)
+// and the activation d / -s (BM x 4) are staged in LDS, then every wave runs,
+// per 32-column sub-block,
 //     I = mfma_i32_16x16x32_i8(A = q, B = codes, C = -s)     (exact int32)
 //     blk += d[m][s] * (float)I
 // and per block acc += fp16(scale[n]) * blk.
@@ -15,7 +23,8 @@
 // k = 8*(l/16) .. +7; the codes for columns 8t..8t+7 of a sub-block are the
 // 2-bit fields {2(t%2), 2(t%2)+1} of its word t/2, so each lane unpacks its
 // B fragment with two shift+mask ops. C row 4*(l/16)+r, column l%16 lands in
-// accumulator r of lane l.
+// accumulator r of lane l. The other kernels map the codes 0 / 1 / 2 to int8
+// -1 / 0 / +1 (one byte permute per word) and start the accumulator at 0.
 #include <climits>
 
 #include "../../include/btf/hip_abi.h"
@@ -1000,7 +1009,7 @@ void by_mode_pf2(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
 
 template <int MT, bool DUMP>
 void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
-  constexpr int KB = MT >= 4 ? 1 : 8;
+  constexpr int KB = MT >= 4 ? 1 : 8;  // 8 blocks per round for one or two activation tiles
   if (mode == BTF_GEMV_STORE)
     hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
   else if (mode == BTF_GEMV_ADD)
@@ -1080,12 +1089,8 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
       by_mode_pf<2>(mode, a, dim3(tiles, (nb + 63) / 64), st);
     return launch_status("gemm_pf_kernel");
   }
-  if (MT == 1)
-    dmp ? by_mode<1, true>(mode, a, grid, st) : by_mode<1, false>(mode, a, grid, st);
-  else if (MT == 2)
-    dmp ? by_mode<2, true>(mode, a, grid, st) : by_mode<2, false>(mode, a, grid, st);
-  else
-    dmp ? by_mode<4, true>(mode, a, grid, st) : by_mode<4, false>(mode, a, grid, st);
+  // left: the exact-I dump (btf_hip_gemv_i32_dump) of more than 32 rows
+  by_mode<4, true>(mode, a, grid, st);
   return launch_status("gemm_mfma_kernel");
 }
 

@@ -211,9 +211,10 @@ def path(request, hip):
 
 
 @pytest.mark.parametrize("K,M", [(1024, 1), (1024, 3), (1024, 8), (1024, 13), (5120, 1), (5120, 4),
-                                 (17408, 1), (17408, 2), (2048, 32)])
+                                 (17408, 1), (17408, 2), (2048, 32), (1024, 40)])
 def test_gemv_i32_bit_exact(hip, oracle, path, K, M):
-    """The int32 sub-block accumulators are bit-exact on both kernel paths."""
+    """The int32 sub-block accumulators are bit-exact on both kernel paths
+    (MFMA: the K-split tile up to 32 rows, the 64-row tile above)."""
     rng = np.random.default_rng(K * 31 + M)
     N = 37
     codes, scales = random_mat(oracle, rng, N, K)
