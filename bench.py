@@ -818,7 +818,12 @@ def main():
         dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
         d = per[dom]
         if step.M <= 32:
-            tr = traffic_tab.get(f"{engine}/{dom}") if step.M == 1 and args.workload == "sweep" else None
+            if step.M == 1 and args.workload == "sweep":
+                tr = traffic_tab.get(f"{engine}/{dom}")
+            elif args.workload == "batched" and not args.mfma_min_m:
+                tr = traffic_tab.get(f"batched{step.M}/{dom}")  # measured at the default crossover
+            else:
+                tr = None
             roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                     "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
                     "traffic_source": tr["source"] if tr else None,
