@@ -317,26 +317,33 @@ class Step:
 
 
 def time_graph(hip, torch, fn, reps, warmup):
-    """Capture fn(stream) in one graph, replay warmup + reps times; returns ms per replay."""
+    """Capture fn(stream) in one graph, replay warmup + reps times; returns ms
+    per replay. The graph and the events are released before returning."""
     s = torch.cuda.Stream()
-    with torch.cuda.stream(s):
-        fn(s.cuda_stream)  # eager pass (first-launch costs outside the graph)
+    g, e0, e1 = None, None, None
+    try:
+        with torch.cuda.stream(s):
+            fn(s.cuda_stream)  # eager pass (first-launch costs outside the graph)
+            s.synchronize()
+            g = hip.Graph(s)
+            with g:
+                fn(s.cuda_stream)
+            for _ in range(warmup):
+                g.launch()
+            s.synchronize()
+            e0, e1 = hip.Event(), hip.Event()
+            torch.cuda.synchronize()
+            e0.record(s)
+            for _ in range(reps):
+                g.launch()
+            e1.record(s)
+            s.synchronize()
+            return e0.elapsed_ms(e1) / reps
+    finally:
         s.synchronize()
-        g = hip.Graph(s)
-        with g:
-            fn(s.cuda_stream)
-        for _ in range(warmup):
-            g.launch()
-        s.synchronize()
-        e0, e1 = hip.Event(), hip.Event()
-        torch.cuda.synchronize()
-        e0.record(s)
-        for _ in range(reps):
-            g.launch()
-        e1.record(s)
-        s.synchronize()
-        ms = e0.elapsed_ms(e1) / reps
-    return ms, g
+        for o in (e0, e1, g):
+            if o is not None:
+                o.close()
 
 
 def time_program(hip, torch, prog, reps, warmup):
@@ -347,14 +354,19 @@ def time_program(hip, torch, prog, reps, warmup):
         prog.launch(s.cuda_stream)
     s.synchronize()
     e0, e1 = hip.Event(), hip.Event()
-    e0.record(s)
-    for _ in range(reps):
-        prog.launch(s.cuda_stream)
-    e1.record(s)
-    s.synchronize()
-    if prog.error():
-        raise RuntimeError("step program reported a timeout")
-    return e0.elapsed_ms(e1) / reps
+    try:
+        e0.record(s)
+        for _ in range(reps):
+            prog.launch(s.cuda_stream)
+        e1.record(s)
+        s.synchronize()
+        if prog.error():
+            raise RuntimeError("step program reported a timeout")
+        return e0.elapsed_ms(e1) / reps
+    finally:
+        s.synchronize()
+        e0.close()
+        e1.close()
 
 
 def verify_vs_graph(torch, step: Step, runner):
@@ -377,68 +389,84 @@ def verify_vs_graph(torch, step: Step, runner):
     return True, "bit-exact"
 
 
+def cpu_info():
+    """(model string, logical CPUs this process may run on, logical CPUs of the host)."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except AttributeError:
+        allowed = os.cpu_count() or 1
+    return model, allowed, os.cpu_count() or allowed
+
+
 def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
-    """The reference CPU emulator's GEMV (or the oracle port) on a bounded sample
-    of the same workload: the projections of the first layers, M rows."""
+    """The reference CPU emulator's GEMV (or the oracle port) on a bounded
+    sample of the same workload: the projections of the first layers, M rows,
+    each with its Q8 quantize. Threads as the reference's bd::ThreadPool(0)
+    (ref/bonsai-decoder/src/cpu_ops.cpp:19-21): every CPU the process may run
+    on, no cap; then the same sample on one thread. budget_s is split 2:1
+    between the two runs."""
     import numpy as np
     sys.path.insert(0, ORACLE)
     from btf_oracle import Oracle, Ref, have_ref
     O = Oracle()
     kind = "reference" if have_ref() else "port"
     R = Ref() if kind == "reference" else None
-    try:
-        threads = len(os.sched_getaffinity(0))
-    except AttributeError:
-        threads = os.cpu_count() or 1
-    threads = max(1, min(16, threads))
+    model, allowed, logical = cpu_info()
     M = step.M
     rng = np.random.default_rng(0)
     xe = rng.standard_normal((M, E)).astype(np.float32)
     qe, de, se = O.quantize_rows(xe)
     xf = rng.standard_normal((M, F)).astype(np.float32)
     qf, df, sf = O.quantize_rows(xf)
-    total_t, total_b, layers_done = 0.0, 0, 0
-    cpu_model = ""
-    try:
-        with open("/proc/cpuinfo") as fh:
-            for line in fh:
-                if line.startswith("model name"):
-                    cpu_model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     # Host copies of up to 8 layers (about 750 MB, well beyond the host's
     # caches), cycled until the time budget is spent.
     nl = min(step.layers, 8)
     names = (("qkv", E), ("o", E), ("gate", E), ("up", E), ("down", F))
     host = {(name, l): S.host_mat(name, l) for l in range(nl) for name, _ in names}
-    l = 0
-    while total_t < budget_s:
-        for name, K in names:
-            codes, scales = host[(name, l % nl)]
-            q, d, s_ = (qe, de, se) if K == E else (qf, df, sf)
-            t0 = time.perf_counter()
-            O.quantize_rows(xe if K == E else xf)  # the Q8 quantize of the input
-            tq = time.perf_counter() - t0
-            if R is not None:
-                t, _ = R.emu_gemv_timed(codes, scales, K, q, d, s_, reps=1, threads=threads)
-            else:
+
+    def run(threads, budget):
+        total_t, total_b, sets, l = 0.0, 0, 0, 0
+        while total_t < budget:
+            for name, K in names:
+                codes, scales = host[(name, l % nl)]
+                q, d, s_ = (qe, de, se) if K == E else (qf, df, sf)
                 t0 = time.perf_counter()
-                O.gemv(codes, scales, K, q, d, s_, nthreads=threads)
-                t = time.perf_counter() - t0
-            N = codes.shape[0]
-            total_t += t + tq
-            total_b += gemv_bytes(N, K, M) + prep_bytes(K, M)
-        layers_done += 1
-        l += 1
-    gbs = total_b / total_t / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": threads, "kind": kind,
-            "tok_s_equiv": round(total_b / total_t / step.total_bytes, 4) if M == 1 else None,
-            "sample": f"{layers_done} layer GEMV set(s), cycling over {nl} distinct layers, "
-                      f"x (QKV 5120->7168, o 5120->5120, gate/up 5120->17408, "
-                      f"down 17408->5120), M={M}, each GEMV with its Q8 quantize; "
-                      f"{'reference EmuDecoder::gemv (src/emu_decoder.cpp:143-165) built from the reference sources' if kind == 'reference' else 'oracle port of EmuDecoder::gemv'}, "
-                      f"{total_t:.2f} s of CPU time; host CPU: {cpu_model}"}
+                O.quantize_rows(xe if K == E else xf)  # the Q8 quantize of the input
+                tq = time.perf_counter() - t0
+                if R is not None:
+                    t, _ = R.emu_gemv_timed(codes, scales, K, q, d, s_, reps=1, threads=threads)
+                else:
+                    t0 = time.perf_counter()
+                    O.gemv(codes, scales, K, q, d, s_, nthreads=threads)
+                    t = time.perf_counter() - t0
+                total_t += t + tq
+                total_b += gemv_bytes(codes.shape[0], K, M) + prep_bytes(K, M)
+            sets += 1
+            l += 1
+        return total_b / total_t / 1e9, sets, total_t
+
+    gbs, sets, tt = run(allowed, budget_s * 2 / 3)
+    gbs1, sets1, tt1 = run(1, budget_s / 3)
+    what = ("reference EmuDecoder::gemv (src/emu_decoder.cpp:143-165) built from the reference sources"
+            if kind == "reference" else "oracle port of EmuDecoder::gemv")
+    return {"value": round(gbs, 3), "unit": "GB/s", "cores": allowed, "kind": kind,
+            "tok_s_equiv": round(gbs * 1e9 / step.total_bytes, 4) if M == 1 else None,
+            "value_1_thread": round(gbs1, 3),
+            "tok_s_equiv_1_thread": round(gbs1 * 1e9 / step.total_bytes, 4) if M == 1 else None,
+            "cpu_model": model, "logical_cpus_allowed": allowed, "logical_cpus_host": logical,
+            "sample": f"{sets} layer GEMV set(s) on {allowed} threads ({tt:.2f} s) and {sets1} on 1 thread "
+                      f"({tt1:.2f} s), cycling over {nl} distinct layers x (QKV 5120->7168, o 5120->5120, "
+                      f"gate/up 5120->17408, down 17408->5120), M={M}, each GEMV with its Q8 quantize; {what}; "
+                      f"host CPU: {model}, {allowed} of {logical} logical CPUs allowed"}
 
 
 def write_synth_gguf(path, layers, seed=0, chunk=1 << 26):
@@ -577,6 +605,8 @@ def run_load(args, hip, torch):
     rep_gbs = 5 * nbytes / (e0.elapsed_ms(e1) * 1e-3) / 1e9
     log(f"stages on a {nbytes / 2**20:.0f} MiB slice: host copy from the mapping {host_gbs:.2f} GB/s, "
         f"copy engine {dma_gbs:.2f} GB/s, repack kernel {rep_gbs:.1f} GB/s (of PTQ1_0 read)")
+    e0.close()
+    e1.close()
     g.close()
     cpu = None
     if not args.no_cpu:
@@ -705,7 +735,10 @@ def main():
         if not ok:
             raise SystemExit(f"step program does not match the op-by-op launches: {why}")
         step.reset()
-        engine_ms["step"] = time_program(hip, torch, prog, args.steps, args.warmup)
+        try:
+            engine_ms["step"] = time_program(hip, torch, prog, args.steps, args.warmup)
+        finally:
+            prog.close()
         log(f"step engine: {engine_ms['step']:.4f} ms per step")
     if "chain" in engines:
         ok, why = verify_vs_graph(torch, step, lambda st: step.run_chain(st))
@@ -714,11 +747,11 @@ def main():
         if not ok:
             raise SystemExit(f"chain launches do not match the op-by-op launches: {why}")
         step.reset()
-        engine_ms["chain"], _ = time_graph(hip, torch, step.run_chain, args.steps, args.warmup)
+        engine_ms["chain"] = time_graph(hip, torch, step.run_chain, args.steps, args.warmup)
         log(f"chain engine: {engine_ms['chain']:.4f} ms per step")
     if "graph" in engines:
         step.reset()
-        engine_ms["graph"], g = time_graph(hip, torch, step.run, args.steps, args.warmup)
+        engine_ms["graph"] = time_graph(hip, torch, step.run, args.steps, args.warmup)
         log(f"graph engine: {engine_ms['graph']:.4f} ms per step")
     # The same chain on the PTQ1_0 rows read directly (btf_hip_launch_gemv_ptq1_0
     # in a graph of quantize + GEMV launches): checked bit-exact against the
@@ -730,7 +763,7 @@ def main():
         if not ok:
             raise SystemExit(f"PTQ1_0-direct launches do not match the op-by-op launches: {why}")
         step.reset()
-        b3_ms, _ = time_graph(hip, torch, step.run_b3, args.steps, args.warmup)
+        b3_ms = time_graph(hip, torch, step.run_b3, args.steps, args.warmup)
         b3 = {"ms_per_step": round(b3_ms, 4), "bytes_per_step": step.b3_total_bytes,
               "GBs": round(step.b3_total_bytes / (b3_ms / 1e3) / 1e9, 1), "tok_s_equiv": round(1e3 / b3_ms, 2),
               "verified": why, "kinds": {}}
@@ -739,7 +772,7 @@ def main():
             reps = 1 if kind == "output" else layers
             fn = (lambda st, kind=kind: step.kind_launch_b3(kind, 0, st)) if kind == "output" else \
                  (lambda st, kind=kind: [step.kind_launch_b3(kind, l, st) for l in range(layers)])
-            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            kms = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
             avg_us = kms * 1e3 / reps
             bb = step.kind_bytes_b3[kind]
             b3["kinds"][kind] = {"avg_us": round(avg_us, 3), "bytes": bb, "GBs": round(bb / (avg_us * 1e-6) / 1e9, 1)}
@@ -761,7 +794,7 @@ def main():
             reps = 1 if kind == "output" else layers
             fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st, fk)) if kind == "output" else \
                  (lambda st, kind=kind: [step.kind_launch(kind, l, st, fk) for l in range(layers)])
-            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            kms = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
             avg_us = kms * 1e3 / reps
             b = step.kind_bytes[kind]
             per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
@@ -791,7 +824,7 @@ def main():
         }
         ends = {}
         for name, fn in fns.items():
-            kms, _ = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
+            kms = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
             ends[f"{name}_us"] = round(kms * 1e3 / 64, 3)
         ends["embed_bytes"] = E // 4 + E // 64 + 4 * E
         ends["argmax_bytes"] = 4 * V

@@ -17,6 +17,7 @@ from __future__ import annotations
 import ctypes as C
 import enum
 import os
+import sys
 from dataclasses import dataclass
 
 HERE = os.path.dirname(os.path.abspath(__file__))
@@ -185,6 +186,16 @@ def _stream(st):
 def _check(rc: int):
     if rc != BTF_OK:
         raise RuntimeError(_last_error().decode() or f"btf_hip error {rc}")
+
+
+def _finalize(obj):
+    """Release a handle from __del__, except at interpreter shutdown: then the
+    HIP runtime (and a profiler attached to it) may already be torn down, and
+    the process exit releases the device memory anyway. Owners that need a
+    deterministic release call close() themselves."""
+    if sys.is_finalizing():
+        return
+    obj.close()
 
 
 @dataclass
@@ -404,7 +415,7 @@ class StepProgram:
             self.h = None
 
     def __del__(self):
-        self.close()
+        _finalize(self)
 
 
 def step_create_raw(vecs, gemvs) -> int:
@@ -452,10 +463,13 @@ class Graph:
     def launch(self):
         _check(_graph_launch(self.exec, self.stream))
 
-    def __del__(self, _destroy=_graph_destroy):
-        if self.exec:
+    def close(self, _destroy=_graph_destroy):
+        if getattr(self, "exec", None):
             _destroy(self.exec)
             self.exec = None
+
+    def __del__(self):
+        _finalize(self)
 
 
 class Event:
@@ -474,10 +488,13 @@ class Event:
         _check(_event_elapsed(C.byref(ms), self.h, end.h))
         return ms.value
 
-    def __del__(self, _destroy=_event_destroy):
+    def close(self, _destroy=_event_destroy):
         if getattr(self, "h", None):
             _destroy(self.h)
             self.h = None
+
+    def __del__(self):
+        _finalize(self)
 
 
 class MappedHostBuffer:
@@ -493,12 +510,12 @@ class MappedHostBuffer:
         return np.ctypeslib.as_array((C.c_uint8 * self.nbytes).from_address(self.host))
 
     def close(self, _free=_host_free):
-        if self.host:
+        if getattr(self, "host", None):
             _free(self.host)
             self.host = None
 
     def __del__(self):
-        self.close()
+        _finalize(self)
 
 
 GGUF_STRING, GGUF_ARRAY, GGUF_F32, GGUF_F64 = 8, 9, 6, 12
@@ -615,7 +632,7 @@ class Gguf:
             self.h = None
 
     def __del__(self):
-        self.close()
+        _finalize(self)
 
 
 def ggml_row_bytes(ggml_type: int, n: int) -> int:
@@ -661,7 +678,7 @@ class Loader:
             self.h = None
 
     def __del__(self):
-        self.close()
+        _finalize(self)
 
 
 def loader_create_raw(staging_bytes: int) -> int:

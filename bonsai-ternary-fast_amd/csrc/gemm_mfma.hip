@@ -800,16 +800,16 @@ __device__ __forceinline__ void wait_vm() {
 // address lds + 16 l; a 2-byte load fills the low half of the 4-byte slot at
 // lds + 4 l (sub-dword loads keep 4-byte lane slots). Issued as inline assembly so that the compiler's
 // wait insertion does not order every later LDS read behind it; the kernel
-// waits with wait_vm itself. M0 (the LDS base) is set in the same statement,
-// with the one wait state an LDS-direct load needs after an SALU write of M0;
-// the compiler reserves M0 and no other code of the kernel reads it (checked
-// in its assembly: every M0 write is one of these).
+// waits with wait_vm itself. The LDS base is an input bound to M0 (the
+// "{m0}" constraint): the compiler writes M0 itself and knows what it holds;
+// the statement adds the one wait state an LDS-direct load needs after an
+// SALU write of M0.
 __device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 __device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ushort %0, off" : : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds))
+  asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 

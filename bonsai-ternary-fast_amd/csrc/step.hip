@@ -139,9 +139,9 @@ constexpr int kRecSlots = 3;  // records of ops i, i + 1, i + 2 (slot = op index
 
 struct Lds {
   OpDev opd[kMaxOps];        // the program
-  uint32_t act_q[2][kMaxK / 4];  // q bytes of an op's input (by op parity)
-  float act_d[2][kMaxK / 32];    // d / 16
-  int32_t act_s[2][kMaxK / 32];  // -16 s
+  // An op's Q8 input (by op parity) as the image of its LL words: per
+  // 32-value block 8 words of q bytes, d (f32 bits), s.
+  uint32_t act[2][kMaxK / 32 * kWordsPerBlock];
   float part[kMaxPart];       // [1024-column slice][local row]
   float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
   uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
@@ -227,19 +227,8 @@ __device__ __forceinline__ void fetch_words(const OpDev& op, Lds& L, int lane, C
         if (pending & (1u << b)) v[b] = ll_load(in + at[b]);
     }
 #pragma unroll
-    for (int b = 0; b < kFB; ++b) {
-      const int idx = at[b];
-      if (idx >= 0) {
-        const uint32_t data = (uint32_t)v[b];
-        const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
-        if (w < 8)
-          L.act_q[ob][blk * 8 + w] = data;
-        else if (w == 8)
-          L.act_d[ob][blk] = __uint_as_float(data) * 0.0625f;  // exact: the dot returns 16 * I
-        else
-          L.act_s[ob][blk] = -16 * (int32_t)data;
-      }
-    }
+    for (int b = 0; b < kFB; ++b)
+      if (at[b] >= 0) L.act[ob][at[b]] = (uint32_t)v[b];
   }
 }
 
@@ -287,16 +276,7 @@ __device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t 
 #pragma unroll
   for (int b = 0; b < kEIn; ++b) {
     const int idx = lid + b * kIL;
-    if (idx < nin) {
-      const uint32_t data = (uint32_t)f.v[b];
-      const int blk = idx / kWordsPerBlock, w = idx - blk * kWordsPerBlock;
-      if (w < 8)
-        L.act_q[ob][blk * 8 + w] = data;
-      else if (w == 8)
-        L.act_d[ob][blk] = __uint_as_float(data) * 0.0625f;
-      else
-        L.act_s[ob][blk] = -16 * (int32_t)data;
-    }
+    if (idx < nin) L.act[ob][idx] = (uint32_t)f.v[b];
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the input words are in LDS
   if ((lid & 63) == 0) __hip_atomic_store(&L.early_seq[lid >> 6], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -520,27 +500,26 @@ __device__ __forceinline__ void issue_entry(const OpLd& d, const LaneOff& lo, co
   sl.s = __builtin_amdgcn_raw_buffer_load_b32(hi ? d.shi : d.slo, (int)lo.s, (int)os, kNT);
 }
 
-// The activation of this lane's chunk of slice s: 64 q bytes, and per
-// sub-block d/16 and -16 s (stored so by the input fetch). The 4 row groups of a
-// wave read the same addresses (LDS broadcasts).
+// The activation of this lane's chunk of slice s (64 columns = two Q8
+// blocks): 64 q bytes, and per sub-block d/16 and -16 s (the dot returns
+// 16 * I; both conversions are exact). The 4 row groups of a wave read the
+// same addresses (LDS broadcasts).
 __device__ __forceinline__ void load_act(const Lds& L, int ob, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
                                          int (&an)[2]) {
-  const int chunk = s * 16 + l16;
-  const u32x4* qp = reinterpret_cast<const u32x4*>(&L.act_q[ob][chunk * 16]);
+  const int blk = 2 * (s * 16 + l16);
+  const uint2* p = reinterpret_cast<const uint2*>(&L.act[ob][blk * kWordsPerBlock]);  // 8-byte aligned
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const u32x4 v = qp[i];
-    aq[4 * i] = v.x;
-    aq[4 * i + 1] = v.y;
-    aq[4 * i + 2] = v.z;
-    aq[4 * i + 3] = v.w;
+  for (int h = 0; h < 2; ++h) {  // block blk + h: words 10 h .. 10 h + 9
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint2 v = p[5 * h + i];
+      aq[8 * h + 2 * i] = v.x;
+      aq[8 * h + 2 * i + 1] = v.y;
+    }
+    const uint2 ds = p[5 * h + 4];
+    ad[h] = __uint_as_float(ds.x) * 0.0625f;
+    an[h] = -16 * (int)ds.y;
   }
-  const float2 d = *reinterpret_cast<const float2*>(&L.act_d[ob][2 * chunk]);
-  const int2 sv = *reinterpret_cast<const int2*>(&L.act_s[ob][2 * chunk]);
-  ad[0] = d.x;
-  ad[1] = d.y;
-  an[0] = sv.x;
-  an[1] = sv.y;
 }
 
 // 16 * (code . q - s) over the two 32-column sub-blocks of a 16-byte chunk,
@@ -654,15 +633,6 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     for (int r = 0; r < kRing; ++r) issue_entry(ld_cur, lo_cur, a, r, ring[r]);
   }
   for (;;) {
-    // the next op's first batch (past the program's end: this op's matrices)
-    OpLd ld_nxt = ld_cur;
-    BAddr a_nxt;
-    {
-      const OpWork nw = op_work(L, wave, cur.next);
-      if (cur.next < nops) ld_nxt = op_ld(L, cur.next);
-      a_nxt = batch_addr(ld_nxt, nw.first, G, BPos{nw.u0, nw.s0, nw.q0});
-    }
-    const LaneOff lo_nxt = lane_off(ld_nxt, l16, grp);
     const int ob = cur.i & 1;  // LDS buffers of this op
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
@@ -694,14 +664,9 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     int an[2];
     load_act(L, ob, cp.s, l16, aq, ad, an);
     const int nb = cur.P / kRing;
-    for (int b = 0; b < nb; ++b) {
-      // refills: the next batch of this op, or in the last batch the next op's first
-      BPos np = cp;
-      bpos_next(cur.qlog, cur.S, np);
-      const bool last = b == nb - 1;
-      const OpLd& ld = last ? ld_nxt : ld_cur;
-      const LaneOff lo = last ? lo_nxt : lo_cur;
-      const BAddr a = last ? a_nxt : batch_addr(ld_cur, cur.first, G, np);
+    // One batch: consume ring slot r, refill it with entry r of the batch at
+    // `a` (loads through `ld` / `lo`), then the batch's row sums and count.
+    auto run_batch = [&](int b, const OpLd& ld, const LaneOff& lo, const BAddr& a, const BPos& np, bool last) {
       float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
@@ -729,12 +694,26 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
       }
       if (!last && np.s != cp.s) load_act(L, ob, np.s, l16, aq, ad, an);
       cp = np;
+    };
+    for (int b = 0; b < nb - 1; ++b) {  // refills: the next batch of this op
+      BPos np = cp;
+      bpos_next(cur.qlog, cur.S, np);
+      run_batch(b, ld_cur, lo_cur, batch_addr(ld_cur, cur.first, G, np), np, false);
+    }
+    {
+      // the last batch refills with the next op's first batch (past the
+      // program's end: this op's matrices again). Its addresses are formed
+      // only here, so they hold no registers through the op's other batches.
+      const OpWork nw = op_work(L, wave, cur.next);
+      if (cur.next < nops) {
+        ld_cur = op_ld(L, cur.next);
+        lo_cur = lane_off(ld_cur, l16, grp);
+      }
+      run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nw.first, G, BPos{nw.u0, nw.s0, nw.q0}), cp, true);
     }
     lds_barrier();  // B: every wave is done with the op
     if (cur.next >= nops) break;
     cur = op_work(L, wave, cur.next);
-    ld_cur = ld_nxt;
-    lo_cur = lo_nxt;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the trailing dummy loads
 }
@@ -951,7 +930,11 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
   // arrive advances the epoch for the next launch (it is read before any
   // workgroup of this launch can have finished its first op).
   lds_barrier();
-  if (threadIdx.x == 0) {
+  // (the thread index is re-read here: a lane mask computed at the start
+  // would hold two SGPRs through the whole kernel)
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  if (tid == 0) {
     const uint32_t prev = __hip_atomic_fetch_add(&ctl->done, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev == (uint32_t)G - 1) {
       __hip_atomic_store(&ctl->done, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1272,14 +1255,15 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
   // before that previous GEMV (a workgroup then never waits for its own
   // unpublished output). An add-mode op whose old value was produced by the
   // previous GEMV with the same unit placement takes it from the LDS carry
-  // (the same workgroup computed it).
+  // (the same workgroup computed it) -- unless that GEMV is a swiglu, whose
+  // epilogue keeps its rows in another layout and writes no carry.
   {
     int pd = -1;  // previous GEMV in program order
     for (int d = 0; d < (int)ops.size(); ++d) {
       OpDev& o = ops[d];
       if (o.kind != 1) continue;
-      if (o.mode == BTF_GEMV_ADD && pd >= 0 && (int)o.old_tag - 1 == pd && ops[pd].units == o.units &&
-          ops[pd].rot == o.rot) {
+      if (o.mode == BTF_GEMV_ADD && pd >= 0 && (int)o.old_tag - 1 == pd && ops[pd].mode != BTF_GEMV_SWIGLU &&
+          ops[pd].units == o.units && ops[pd].rot == o.rot) {
         o.carry_in = 1;
         ops[pd].carry_out = 1;
       }

@@ -2,8 +2,9 @@
 // with the reference's own CPU sources, read where they lie in the reference
 // checkout (nothing is copied), into oracle/_ref/libbtf_ref.so. It exposes the
 // reference's functions through a C ABI so tests can pin the oracle
-// (btf_oracle.c) against the real code. Only tests/golden/make_golden.py and
-// the CPU tests load it; it never travels into the product library.
+// (btf_oracle.c) against the real code. tests/golden/make_golden.py, the CPU
+// tests and bench.py's CPU-baseline leg (which times the reference emulator's
+// GEMV) load it; it never links into the product library.
 //
 // EmuDecoder (src/emu_decoder.cpp) keeps gemv() and prep() private inside an
 // anonymous namespace, so this translation unit includes that source file and

@@ -281,6 +281,64 @@ def test_gemv_27b_shapes_batch1(hip, oracle, K, N):
     assert np.array_equal(host(out), I_ref)
 
 
+def test_gemv_27b_gate_up_swiglu_batch1(hip, oracle):
+    """Config 2's gate/up pair at full shape (5120 -> 2 x 17408) as one
+    swiglu launch at M = 1, on the seeded generator's weights: silu(g) * u
+    within 1e-3 of the oracle; I bit-exact on the first and last 64 rows of
+    both matrices."""
+    K, N = 5120, 17408
+    gate = gen_mat(oracle, 0, 5 * 7 + 2, N, K)
+    up = gen_mat(oracle, 0, 5 * 7 + 3, N, K)
+    rng = np.random.default_rng(11)
+    _, q, d, s = random_act(oracle, rng, 1, K)
+    ref = oracle.swiglu(oracle.gemv(gate[0], gate[1], K, q, d, s), oracle.gemv(up[0], up[1], K, q, d, s))
+    torch = _torch()
+    h = zeros((1, N), torch.float32)
+    act = q8_dev(q, d, s, hip)
+    hip.launch_gemv([hip.GemvSeg(dev(gate[0]), dev(gate[1]), N, h, N), hip.GemvSeg(dev(up[0]), dev(up[1]), N, None, 0)],
+                    K, 1, act, hip.GemvMode.kSwiglu, stream())
+    assert_close_1e3(host(h), ref, "gate/up swiglu 5120->17408")
+    for codes in (gate[0], up[0]):
+        for rows in (slice(0, 64), slice(N - 64, N)):
+            sub = np.ascontiguousarray(codes[rows])
+            out = zeros((1, 64, K // 32), torch.int32)
+            hip.gemv_i32_dump(dev(sub), 64, K, 1, act, out, stream())
+            assert np.array_equal(host(out), oracle.gemv_i32(sub, K, q, s))
+
+
+# The layer's projections at full shape (config 3): (kind, K, N, mode)
+LAYER_KINDS = [("qkv", 5120, 7168, "store"), ("o", 5120, 5120, "add"), ("gateup", 5120, 17408, "swiglu"),
+               ("down", 17408, 5120, "add")]
+
+
+@pytest.mark.parametrize("M", [8, 32])
+@pytest.mark.parametrize("kind,K,N,mode", LAYER_KINDS)
+def test_gemm_27b_layer_shapes_batched(hip, oracle, kind, K, N, mode, M):
+    """Batched decode on every projection of a 27B layer at full shape, on
+    the seeded generator's weights, against the oracle (add mode onto a
+    random residual; swiglu as one gate+up launch)."""
+    mid = 1000 + LAYER_KINDS.index((kind, K, N, mode)) * 2
+    W = gen_mat(oracle, 0, mid, N, K)
+    rng = np.random.default_rng(M * 31 + K)
+    _, q, d, s = random_act(oracle, rng, M, K)
+    torch = _torch()
+    act = q8_dev(q, d, s, hip)
+    G = hip.GemvMode
+    if mode == "swiglu":
+        U = gen_mat(oracle, 0, mid + 1, N, K)
+        ref = oracle.swiglu(oracle.gemv(W[0], W[1], K, q, d, s), oracle.gemv(U[0], U[1], K, q, d, s))
+        y = zeros((M, N), torch.float32)
+        hip.launch_gemv([hip.GemvSeg(dev(W[0]), dev(W[1]), N, y, N), hip.GemvSeg(dev(U[0]), dev(U[1]), N, None, 0)],
+                        K, M, act, G.kSwiglu, stream())
+    else:
+        y0 = rng.standard_normal((M, N)).astype(np.float32) if mode == "add" else np.zeros((M, N), np.float32)
+        ref = oracle.gemv(W[0], W[1], K, q, d, s, y=y0.copy(), add=mode == "add")
+        y = dev(y0)
+        hip.launch_gemv([hip.GemvSeg(dev(W[0]), dev(W[1]), N, y, N)], K, M, act,
+                        G.kAdd if mode == "add" else G.kStore, stream())
+    assert_close_1e3(host(y), ref, f"{kind} M={M}")
+
+
 @pytest.mark.parametrize("M", [4, 8, 16, 32, 512])
 def test_gemm_batched_and_prefill(hip, oracle, M):
     """Config-3/4 batch sizes on a 5120-wide layer slice (N = 256)."""
