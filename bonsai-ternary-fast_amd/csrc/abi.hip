@@ -198,10 +198,7 @@ int btf_hip_launch_embed(const uint8_t* codes, const uint16_t* scales, const int
   return embed(codes, scales, d_tok, M, E, block, inv ? inv->signs : nullptr, x, static_cast<hipStream_t>(stream));
 }
 
-int64_t btf_hip_argmax_part_bytes(int V) {
-  (void)V;
-  return argmax_part_bytes();
-}
+int64_t btf_hip_argmax_part_bytes(int V) { return argmax_part_bytes(V); }
 
 int btf_hip_launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t stream) {
   if (!logits || !part || !d_tok_out) return fail(BTF_ERR_ARGS, "argmax: null pointer");

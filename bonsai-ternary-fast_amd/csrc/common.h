@@ -185,7 +185,7 @@ int gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks
                const DevState& ds);
 int embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E, int block, const float* signs,
           float* x, hipStream_t st);
-int64_t argmax_part_bytes();
+int64_t argmax_part_bytes(int V);
 int argmax(const float* logits, int V, void* part, int* out, hipStream_t st);
 int pos_add(int* d_pos, int M, hipStream_t st);
 

@@ -2,174 +2,164 @@
 // the embedding lookup from the packed table with its inverse transform, the
 // greedy pick over the logits, and the position counter.
 //
-//  * embed_kernel: behaviour of the reference's embed_kernel / launch_embed
-//    (src/cuda/kernels.cu:632-662, 886-895) and of its CPU twin, the embedding
-//    step of EmuDecoder::chunk (src/emu_decoder.cpp:171-180) with
-//    bd::hadamard_inverse (ref/bonsai-decoder/src/cpu_ops.cpp:113-118). One
-//    workgroup per (span of S <= 1024 columns, row): the span's code words are
-//    staged in LDS with 4-byte reads (the table may live in mapped host
-//    memory), decoded to (code - 1) * fp16 scale, then the blockwise FWHT runs
-//    in LDS in the CPU's stage order (len = 1, 2, 4, ...), times 1/sqrt(block),
-//    times the signs: bit-exact with the CPU.
-//  * argmax: the greedy pick, smallest index on ties (src/cuda/kernels.cu:
-//    664-704, 897-904; CPU: ref/bonsai-decoder/src/sampler.cpp:20-25). Stage 1:
-//    kArgParts workgroups scan interleaved slices and reduce (value, index)
-//    pairs in the wave with DPP and v_permlane16/32_swap, then across waves in
-//    LDS; stage 2: one workgroup reduces the parts. A NaN logit never wins.
-//  * pos_add: *d_pos += M (src/cuda/kernels.cu:706-708), as a vector atomic.
+//  * embed_slices_kernel: behaviour of the reference's launch_embed
+//    (src/cuda/kernels.cuh:82-85) and of its CPU twin, the embedding step of
+//    EmuDecoder::chunk (src/emu_decoder.cpp:171-180) with bd::hadamard_inverse
+//    (ref/bonsai-decoder/src/cpu_ops.cpp:113-118). One wave per 1024 columns
+//    of a token row, 16 columns per lane: in the T2 layout columns 16 h ..
+//    16 h + 15 of a 128-block are exactly code word h of the block
+//    (include/btf/packed.hpp:35-38), so lane l reads ONE aligned 32-bit word
+//    (the table may be mapped host memory) and the fp16 scale of its block,
+//    decodes 16 values (code - 1) * scale, runs the blockwise FWHT in
+//    registers (slice.h, the CPU's stage order), times 1/sqrt(block), times
+//    the signs. Bit-exact with the CPU. As on the CPU, the signs belong to the
+//    transform (block 0: neither).
+//  * argmax: the greedy pick (src/cuda/kernels.cuh:87-90; CPU:
+//    ref/bonsai-decoder/src/sampler.cpp:20-25). Every logit becomes a 64-bit
+//    key that orders (value, -index) totally: the value's bits in an
+//    order-preserving form in the high word (-0 folded onto +0, a NaN key 0,
+//    below every number), the complement of the index in the low word. The
+//    largest key is the largest value at its smallest index, so the result
+//    does not depend on the order of the reductions. Stage 1: contiguous
+//    2048-value parts, one workgroup each, a max over keys (DPP and
+//    v_permlane16/32_swap in the wave, LDS across waves) into `part`; stage 2:
+//    one wave over the parts. A NaN never wins; all-NaN gives 0.
+//  * pos_add: *d_pos += M, as a vector atomic (src/cuda/kernels.cuh:92).
 #include <cmath>
 
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
+#include "slice.h"
 
 #pragma clang fp contract(off)
 
 namespace btfhip {
 namespace {
 
-constexpr int kEmbedThreads = 256;
+// ---- embedding ----
+constexpr int kEmbedWaves = 4;
 
-__global__ void __launch_bounds__(kEmbedThreads) embed_kernel(const uint8_t* __restrict__ codes,
-                                                               const uint16_t* __restrict__ scales,
-                                                               const int* __restrict__ d_tok, int E, int S, int block,
-                                                               const float* __restrict__ signs, float* __restrict__ x) {
-  extern __shared__ float buf[];                     // S floats
-  __shared__ uint32_t cw[1024 / 16];                 // the span's code words (S / 16)
-  const int m = blockIdx.y, base = blockIdx.x * S;  // E % S == 0, S % 128 == 0
+template <bool VEC>
+__global__ void __launch_bounds__(64 * kEmbedWaves)
+    embed_slices_kernel(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+                        const int* __restrict__ d_tok, int E, int nslices, int block, float hs,
+                        const float* __restrict__ signs, float* __restrict__ x) {
+  const int lane = threadIdx.x & 63;
+  const int sl = blockIdx.x * kEmbedWaves + (threadIdx.x >> 6);
+  if (sl >= nslices) return;  // a whole wave: the butterflies below stay in step
+  const int m = blockIdx.y;
   const size_t tok = (size_t)d_tok[m];
-  const uint32_t* rowc = reinterpret_cast<const uint32_t*>(codes + tok * (size_t)(E / 4) + base / 4);
-  for (int i = threadIdx.x; i < S / 16; i += blockDim.x) cw[i] = rowc[i];
-  __syncthreads();
-  const uint16_t* rows = scales + tok * (size_t)(E / 128);
-  for (int o = threadIdx.x; o < S; o += blockDim.x) {
-    const int e = base + o, eb = e & 127;
-    // T2 address of column eb of a 128-block (include/btf/packed.hpp:35-38)
-    const int byte = (e >> 7) * 32 + (eb >> 5) * 8 + ((eb >> 4) & 1) * 4 + (eb & 3) - base / 4;
-    const int shift = ((eb >> 2) & 3) * 2;
-    const uint32_t c = (cw[byte >> 2] >> ((byte & 3) * 8 + shift)) & 3u;
-    buf[o] = (float)((int)c - 1) * h2f(rows[e >> 7]);
+  const int c0 = sl * kSliceVals + 16 * lane;
+  const bool live = c0 < E;  // E % 128 == 0: whole 128-blocks are live
+  uint32_t w = 0;
+  float sc = 0.f;
+  if (live) {
+    w = reinterpret_cast<const uint32_t*>(codes + tok * (size_t)(E / 4))[c0 >> 4];
+    sc = h2f(scales[tok * (size_t)(E / 128) + (c0 >> 7)]);
   }
-  __syncthreads();
-  float hs = 1.0f;
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {  // column j of the word: byte j % 4, 2-bit field j / 4
+    const int c = (int)((w >> (8 * (j & 3) + 2 * (j >> 2))) & 3u);
+    v[j] = (float)(c - 1) * sc;
+  }
   if (block > 0) {
-    for (int len = 1; len < block; len <<= 1) {
-      for (int p = threadIdx.x; p < (S >> 1); p += blockDim.x) {
-        const int j = (p / len) * (len << 1) + (p % len);
-        const float u = buf[j], w = buf[j + len];
-        buf[j] = u + w;
-        buf[j + len] = u - w;
-      }
-      __syncthreads();
-    }
-    hs = 1.0f / sqrtf((float)block);
+    slice_fwht(v, lane, block);
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = v[j] * hs;
+    if (signs && live)
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = v[j] * signs[c0 + j];
   }
-  for (int o = threadIdx.x; o < S; o += blockDim.x) {
-    float v = buf[o];
-    if (block > 0) v = v * hs;
-    if (signs) v = v * signs[base + o];
-    x[(size_t)m * E + base + o] = v;
+  if (!live) return;
+  float* xo = x + (size_t)m * E + c0;
+  if (VEC) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      reinterpret_cast<f32x4*>(xo)[k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+  } else {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) xo[j] = v[j];
   }
 }
 
-// ---- argmax ----
-constexpr int kArgParts = 128;
+// ---- greedy pick ----
 constexpr int kArgThreads = 256;
 
-__device__ __forceinline__ void arg_better(float& bv, int& bi, float v, int i) {
-  if (v > bv || (v == bv && i < bi)) {
-    bv = v;
-    bi = i;
-  }
-}
-// (value, index) reduction over the 64 lanes; every lane gets the winner.
-__device__ __forceinline__ void wave_arg(float& bv, int& bi) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    float v;
-    int i;
-    switch (k) {  // butterfly inside each 16-lane row
-      case 0: v = dpp_f<0xB1>(bv), i = dpp_i<0xB1>(bi); break;    // quad_perm(1,0,3,2)
-      case 1: v = dpp_f<0x4E>(bv), i = dpp_i<0x4E>(bi); break;    // quad_perm(2,3,0,1)
-      case 2: v = dpp_f<0x141>(bv), i = dpp_i<0x141>(bi); break;  // row_half_mirror
-      default: v = dpp_f<0x140>(bv), i = dpp_i<0x140>(bi); break; // row_mirror
-    }
-    arg_better(bv, bi, v, i);
-  }
-  {  // rows 0 <-> 1, 2 <-> 3
-    const auto rv = __builtin_amdgcn_permlane16_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
-    const auto ri = __builtin_amdgcn_permlane16_swap((uint32_t)bi, (uint32_t)bi, false, false);
-    arg_better(bv, bi, __uint_as_float(rv[0]), (int)ri[0]);
-    arg_better(bv, bi, __uint_as_float(rv[1]), (int)ri[1]);
-  }
-  {  // halves 0 <-> 1
-    const auto rv = __builtin_amdgcn_permlane32_swap(__float_as_uint(bv), __float_as_uint(bv), false, false);
-    const auto ri = __builtin_amdgcn_permlane32_swap((uint32_t)bi, (uint32_t)bi, false, false);
-    arg_better(bv, bi, __uint_as_float(rv[0]), (int)ri[0]);
-    arg_better(bv, bi, __uint_as_float(rv[1]), (int)ri[1]);
-  }
-}
-__device__ __forceinline__ void block_arg(float& bv, int& bi) {
-  __shared__ float rv[kArgThreads / 64];
-  __shared__ int ri[kArgThreads / 64];
-  wave_arg(bv, bi);
-  if ((threadIdx.x & 63) == 0) {
-    rv[threadIdx.x >> 6] = bv;
-    ri[threadIdx.x >> 6] = bi;
-  }
+__global__ void __launch_bounds__(kArgThreads) argmax_parts_kernel(const float* __restrict__ x, int V, int per,
+                                                                   uint64_t* __restrict__ part) {
+  __shared__ uint64_t wk[kArgThreads / 64];
+  const int i0 = blockIdx.x * per, i1 = min(V, i0 + per);
+  uint64_t best = 0;
+  for (int i = i0 + (int)threadIdx.x; i < i1; i += kArgThreads) best = key_max(best, argmax_key(x[i], i));
+  best = wave_max_key(best);
+  if ((threadIdx.x & 63) == 0) wk[threadIdx.x >> 6] = best;
   __syncthreads();
-  bv = -INFINITY;
-  bi = 0x7fffffff;
-  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) arg_better(bv, bi, rv[w], ri[w]);
+  if (threadIdx.x == 0) {
+    uint64_t b = wk[0];
+    for (int w = 1; w < kArgThreads / 64; ++w) b = key_max(b, wk[w]);
+    part[blockIdx.x] = b;
+  }
 }
-
-__global__ void __launch_bounds__(kArgThreads) argmax_parts(const float* __restrict__ x, int V,
-                                                            float2* __restrict__ part) {
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < V; i += gridDim.x * blockDim.x) arg_better(bv, bi, x[i], i);
-  block_arg(bv, bi);
-  if (threadIdx.x == 0) part[blockIdx.x] = make_float2(bv, __int_as_float(bi));
-}
-__global__ void __launch_bounds__(kArgThreads) argmax_final(const float2* __restrict__ part, int n,
-                                                            int* __restrict__ out) {
-  float bv = -INFINITY;
-  int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < n; i += blockDim.x) arg_better(bv, bi, part[i].x, __float_as_int(part[i].y));
-  block_arg(bv, bi);
-  if (threadIdx.x == 0) *out = bi == 0x7fffffff ? 0 : bi;
+__global__ void __launch_bounds__(64) argmax_pick_kernel(const uint64_t* __restrict__ part, int nparts,
+                                                         int* __restrict__ out) {
+  uint64_t best = 0;
+  for (int i = threadIdx.x; i < nparts; i += 64) best = key_max(best, part[i]);
+  best = wave_max_key(best);
+  if (threadIdx.x == 0) *out = argmax_key_index(best);
 }
 
 __global__ void __launch_bounds__(64) pos_add_kernel(int* d_pos, int M) {
   if (threadIdx.x == 0) (void)atomicAdd(d_pos, M);
 }
 
-int span_of(int n) {
-  int s = 1;
-  while (s < 1024 && n % (s * 2) == 0) s *= 2;
-  return s;
-}
-
 }  // namespace
 
 int embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E, int block, const float* signs,
           float* x, hipStream_t st) {
-  const int S = span_of(E);
-  if (S < 128) return fail(BTF_ERR_ARGS, "embed: width must be a multiple of 128");
-  if (block > 0 && S % block) return fail(BTF_ERR_ARGS, "embed: hadamard block does not divide the span");
-  hipLaunchKernelGGL(embed_kernel, dim3(E / S, M), dim3(kEmbedThreads), (size_t)S * sizeof(float), st, codes, scales,
-                     d_tok, E, S, block, signs, x);
-  return launch_status("embed_kernel");
+  int span = 1024;  // the largest power of two <= 1024 dividing E
+  while (E % span) span >>= 1;
+  if (span < 128) return fail(BTF_ERR_ARGS, "embed: width must be a multiple of 128");
+  if (block > 0 && span % block) return fail(BTF_ERR_ARGS, "embed: hadamard block does not divide the span");
+  const int nslices = (E + kSliceVals - 1) / kSliceVals;
+  const float hs = block > 0 ? 1.0f / std::sqrt((float)block) : 1.0f;
+  const dim3 grid((nslices + kEmbedWaves - 1) / kEmbedWaves, M), blk(64 * kEmbedWaves);
+  if ((reinterpret_cast<uintptr_t>(x) & 15) == 0)
+    hipLaunchKernelGGL(embed_slices_kernel<true>, grid, blk, 0, st, codes, scales, d_tok, E, nslices, block, hs,
+                       block > 0 ? signs : nullptr, x);
+  else
+    hipLaunchKernelGGL(embed_slices_kernel<false>, grid, blk, 0, st, codes, scales, d_tok, E, nslices, block, hs,
+                       block > 0 ? signs : nullptr, x);
+  return launch_status("embed_slices_kernel");
 }
 
-int64_t argmax_part_bytes() { return (int64_t)kArgParts * (int64_t)sizeof(float2); }
+namespace {
+constexpr int kArgPer = 2048;    // logits per part
+constexpr int kArgMaxParts = 256;
+int argmax_parts_of(int V, int* per) {
+  int n = (V + kArgPer - 1) / kArgPer;
+  if (n > kArgMaxParts) n = kArgMaxParts;
+  if (n < 1) n = 1;
+  *per = (V + n - 1) / n;
+  return n;
+}
+}  // namespace
+
+int64_t argmax_part_bytes(int V) {
+  int per;
+  return (int64_t)argmax_parts_of(V > 0 ? V : 1, &per) * (int64_t)sizeof(uint64_t);
+}
 
 int argmax(const float* logits, int V, void* part, int* out, hipStream_t st) {
-  hipLaunchKernelGGL(argmax_parts, dim3(kArgParts), dim3(kArgThreads), 0, st, logits, V, static_cast<float2*>(part));
-  int rc = launch_status("argmax_parts");
+  int per;
+  const int n = argmax_parts_of(V, &per);
+  hipLaunchKernelGGL(argmax_parts_kernel, dim3(n), dim3(kArgThreads), 0, st, logits, V, per,
+                     static_cast<uint64_t*>(part));
+  const int rc = launch_status("argmax_parts_kernel");
   if (rc != BTF_OK) return rc;
-  hipLaunchKernelGGL(argmax_final, dim3(1), dim3(kArgThreads), 0, st, static_cast<const float2*>(part), kArgParts,
-                     out);
-  return launch_status("argmax_final");
+  hipLaunchKernelGGL(argmax_pick_kernel, dim3(1), dim3(64), 0, st, static_cast<const uint64_t*>(part), n, out);
+  return launch_status("argmax_pick_kernel");
 }
 
 int pos_add(int* d_pos, int M, hipStream_t st) {

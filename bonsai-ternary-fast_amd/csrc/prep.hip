@@ -1,10 +1,13 @@
 // prep.hip -- activation prep for the ternary matmul (gfx950).
 //
-// Behaviour of the reference's launch_prep / prep_kernel
-// (src/cuda/kernels.cu:147-202, 745-774) and of its CPU twin
-// EmuDecoder::prep (src/emu_decoder.cpp:122-140):
+// Behaviour of the reference's launch_prep (src/cuda/kernels.cuh:40-43) and
+// of its CPU twin EmuDecoder::prep (src/emu_decoder.cpp:122-140) with
+// bd::rmsnorm and bd::hadamard_input (ref/bonsai-decoder/src/cpu_ops.cpp:
+// 90-127):
 //   x [M][ldx] -> [RMSNorm * w] -> tiled->grouped perm -> signs ->
 //   blockwise WHT (x 1/sqrt(block)) -> Q8_0 (q, d, s) per 32 values.
+// As on the CPU, the perm and the signs belong to the transform: with
+// block == 0 neither is applied.
 //
 // Two kernels:
 //  * q8_kernel: no norm and no transform (every quantize feeding a GEMV in the
@@ -13,14 +16,17 @@
 //    include/btf/packed.hpp:117-134: d = fp16_rn(amax/127) (IEEE division),
 //    q = rint(x * (127/amax)) with ties to even, s = sum q. An all-zero block
 //    gets d = +-0 with the sign of its last element, as the CPU loop does.
-//  * prep_kernel<NORM>: the full transform. One workgroup per (span, row),
-//    span S = the largest power of two <= 1024 dividing n; the WHT runs in LDS
-//    with the CPU's stage order (len = 1, 2, 4, ...), so it is bit-exact; the
-//    RMSNorm sum of squares is a fixed-order double tree, so its last bit can
-//    differ from the CPU's sequential double sum (the reference's own GPU
-//    kernel has the same property).
+//  * prep_slices_kernel<NORM, PERM>: the full transform, a wave per
+//    1024-value slice in registers (slice.h): the FWHT runs in the CPU's
+//    stage order, so without the norm the result is bit-exact; the RMSNorm's
+//    double sum of squares is taken in a fixed canonical order (per 32-value
+//    block, then over the blocks), so its last bit can differ from the CPU's
+//    sequential sum (the reference's own GPU kernel differs likewise).
+#include <cmath>
+
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
+#include "slice.h"
 
 #pragma clang fp contract(off)
 
@@ -28,6 +34,7 @@ namespace btfhip {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr size_t kMaxPrepLds = 64 * 1024;  // block sums of squares of one row (normed prep)
 
 // Quantize 8 consecutive values of one Q8 block held by this lane; the 4
 // lanes of a DPP quad hold the block. Returns the two packed q words; d and s
@@ -96,112 +103,95 @@ __global__ void __launch_bounds__(256) q8_kernel(const float* __restrict__ x, in
 }
 
 // ---- full prep ----
+// One workgroup per row, W waves (W = min(16, slices)); wave w takes the
+// 1024-value slices w, w + W, ... of the row in registers (slice.h: lane l
+// holds values 16 l .. 16 l + 15). With the norm, the waves first write the
+// canonical sum of squares of every 32-value block of the row into LDS, and
+// every wave forms the row's scale from them in one fixed order (so the
+// step program, which gathers the same block sums from its producers, gets
+// the same scale bit for bit). Then per slice: gather through the perm,
+// (x * scale) * w, the normed row to xn_out, * signs, the blockwise FWHT in
+// registers, * 1/sqrt(block), the Q8 of each lane pair's block.
 struct PrepArgs {
   const float* x;
-  int ldx, n, S;
+  int ldx, n, nslices;
   const float* normw;
   float eps;
-  int block, perm_hd, perm_nk, perm_rep;
+  int block, hd, nk, rep;  // rep > 1: tiled -> grouped gather
+  float hs;                // 1/sqrtf(block) (block > 0)
   const float* signs;
-  float* xn_out;
+  float* xn;
   int ldxn;
   int8_t* q;
   float* d;
   int32_t* s;
 };
 
-constexpr int kPrepThreads = 256;
-
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-template <bool NORM>
-__global__ void __launch_bounds__(kPrepThreads) prep_kernel(PrepArgs a) {
-  extern __shared__ float buf[];  // S floats
-  __shared__ double red[kPrepThreads / 64];
-  const int m = blockIdx.y;
-  const int base = blockIdx.x * a.S;
+template <bool NORM, bool PERM>
+__global__ void __launch_bounds__(1024) prep_slices_kernel(PrepArgs a) {
+  extern __shared__ double bsum[];  // [n / 32] block sums of squares (NORM)
+  const int m = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
   const float* xr = a.x + (size_t)m * a.ldx;
   float scale = 1.0f;
   if (NORM) {
-    double acc = 0.0;
-    for (int i = threadIdx.x; i < a.n; i += blockDim.x) acc += (double)xr[i] * (double)xr[i];
-    acc = wave_sum_d(acc);
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    double sum = 0.0;
-    for (int w = 0; w < (int)(blockDim.x >> 6); ++w) sum += red[w];
-    const float mean = (float)(sum / (double)a.n);
-    scale = 1.0f / sqrtf(mean + a.eps);
-  }
-  for (int o = threadIdx.x; o < a.S; o += blockDim.x) {
-    const int og = base + o;
-    int src = og;
-    if (a.block > 0 && a.perm_rep > 1) {
-      const int dd = og % a.perm_hd, t = og / a.perm_hd;
-      const int r = t % a.perm_rep, k = t / a.perm_rep;
-      src = dd + a.perm_hd * (k + a.perm_nk * r);
-    }
-    float v = xr[src];
-    if (NORM) v = (v * scale) * a.normw[src];
-    if (a.block > 0 && a.signs) v = v * a.signs[og];
-    buf[o] = v;
-    if (a.xn_out) {
-      float u = xr[og];
-      if (NORM) u = (u * scale) * a.normw[og];
-      a.xn_out[(size_t)m * a.ldxn + og] = u;
-    }
-  }
-  __syncthreads();
-  float hs = 1.0f;
-  if (a.block > 0) {
-    for (int len = 1; len < a.block; len <<= 1) {
-      for (int p = threadIdx.x; p < (a.S >> 1); p += blockDim.x) {
-        const int j = (p / len) * (len << 1) + (p % len);
-        const float u = buf[j], w = buf[j + len];
-        buf[j] = u + w;
-        buf[j + len] = u - w;
-      }
-      __syncthreads();
-    }
-    hs = 1.0f / sqrtf((float)a.block);
-  }
-  // Q8: 4 lanes per 32-value block, 8 values each.
-  const int nlanes = a.S >> 3;
-  for (int l0 = 0; l0 < nlanes; l0 += blockDim.x) {
-    const int l = l0 + threadIdx.x;
-    const bool live = l < nlanes;
-    float v[8];
+    for (int sl = wave; sl < a.nslices; sl += W) {
+      const int c0 = sl * kSliceVals + 16 * lane;
+      float v[16];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float u = live ? buf[8 * l + i] : 0.f;
-      v[i] = a.block > 0 ? u * hs : u;
+      for (int i = 0; i < 16; ++i) v[i] = c0 + i < a.n ? xr[c0 + i] : 0.f;
+      const double bs = pair_sumsq(v);
+      if (!(lane & 1) && c0 < a.n) bsum[c0 >> 5] = bs;
     }
-    uint32_t q0, q1;
+    __syncthreads();
+    scale = norm_scale([&](int i) { return bsum[i]; }, a.n >> 5, a.n, a.eps, lane);
+  }
+  const bool xform = a.block > 0;
+  for (int sl = wave; sl < a.nslices; sl += W) {
+    const int c0 = sl * kSliceVals + 16 * lane;
+    const bool live = c0 < a.n;  // a.n % 32 == 0: a lane pair is all in or all out
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int og = c0 + i;
+      const int src = PERM ? perm_src(og, a.hd, a.nk, a.rep) : og;
+      float u = live ? xr[src] : 0.f;
+      if (NORM) u = (u * scale) * (live ? a.normw[src] : 0.f);
+      v[i] = u;
+    }
+    if (a.xn && live) {
+      float* xo = a.xn + (size_t)m * a.ldxn + c0;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float u = xr[c0 + i];
+        if (NORM) u = (u * scale) * a.normw[c0 + i];
+        xo[i] = u;
+      }
+    }
+    if (xform) {
+      if (a.signs)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) v[i] = v[i] * (live ? a.signs[c0 + i] : 0.f);
+      slice_fwht(v, lane, a.block);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = v[i] * a.hs;
+    }
+    uint32_t qw[4];
     float dd;
     int ss;
-    q8_quad(v, q0, q1, dd, ss);
+    q8_pair(v, lane, qw, dd, ss);
     if (live) {
-      const size_t col = (size_t)base + 8 * l;
-      uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + (size_t)m * a.n + col);
-      qp[0] = q0;
-      qp[1] = q1;
-      if ((l & 3) == 0) {
-        const size_t bi = (size_t)m * (a.n >> 5) + (col >> 5);
+      uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + (size_t)m * a.n + c0);
+      qp[0] = qw[0];
+      qp[1] = qw[1];
+      qp[2] = qw[2];
+      qp[3] = qw[3];
+      if (!(lane & 1)) {
+        const size_t bi = (size_t)m * (a.n >> 5) + (c0 >> 5);
         a.d[bi] = dd;
         a.s[bi] = ss;
       }
     }
   }
-}
-
-int span_of(int n) {
-  int s = 1;
-  while (s < 1024 && n % (s * 2) == 0) s *= 2;
-  return s;
 }
 
 }  // namespace
@@ -220,31 +210,47 @@ int prep(const float* x, int ldx, int M, int n, const float* normw, float eps, i
       hipLaunchKernelGGL(q8_kernel<false>, dim3((unsigned)grid), dim3(256), 0, st, x, ldx, n, lanes, q, d, s);
     return launch_status("q8_kernel");
   }
+  // The transform acts in blocks of `block` values (a power of two) that
+  // must divide the span: the largest power of two <= 1024 dividing n.
+  int span = 1024;
+  while (n % span) span >>= 1;
+  if (block > 0 && span % block) return fail(BTF_ERR_ARGS, "prep: hadamard block does not divide the span");
+  if (normw && (size_t)(n / 32) * sizeof(double) > kMaxPrepLds)
+    return fail(BTF_ERR_ARGS, "prep: width too large for the normed prep (n <= 262144)");
   PrepArgs p{};
   p.x = x;
   p.ldx = ldx;
   p.n = n;
-  p.S = span_of(n);
+  p.nslices = (n + kSliceVals - 1) / kSliceVals;
   p.normw = normw;
   p.eps = eps;
-  p.block = block;
-  p.perm_hd = perm_hd;
-  p.perm_nk = perm_nk;
-  p.perm_rep = perm_rep;
-  p.signs = signs;
-  p.xn_out = xn_out;
+  p.block = block > 0 ? block : 0;
+  const bool perm = block > 0 && perm_rep > 1;
+  p.hd = perm_hd;
+  p.nk = perm_nk;
+  p.rep = perm_rep;
+  p.hs = block > 0 ? 1.0f / std::sqrt((float)block) : 1.0f;
+  p.signs = block > 0 ? signs : nullptr;
+  p.xn = xn_out;
   p.ldxn = ldxn;
   p.q = q;
   p.d = d;
   p.s = s;
-  if (block > 0 && (p.S % block)) return fail(BTF_ERR_ARGS, "prep: hadamard block does not divide the span");
-  const dim3 grid(n / p.S, M);
-  const size_t smem = (size_t)p.S * sizeof(float);
-  if (normw)
-    hipLaunchKernelGGL(prep_kernel<true>, grid, dim3(kPrepThreads), smem, st, p);
-  else
-    hipLaunchKernelGGL(prep_kernel<false>, grid, dim3(kPrepThreads), smem, st, p);
-  return launch_status("prep_kernel");
+  const int waves = p.nslices < 16 ? p.nslices : 16;
+  const size_t lds = normw ? (size_t)(n / 32) * sizeof(double) : 0;
+  const dim3 grid(M), blk(64 * waves);
+  if (normw) {
+    if (perm)
+      hipLaunchKernelGGL((prep_slices_kernel<true, true>), grid, blk, lds, st, p);
+    else
+      hipLaunchKernelGGL((prep_slices_kernel<true, false>), grid, blk, lds, st, p);
+  } else {
+    if (perm)
+      hipLaunchKernelGGL((prep_slices_kernel<false, true>), grid, blk, 0, st, p);
+    else
+      hipLaunchKernelGGL((prep_slices_kernel<false, false>), grid, blk, 0, st, p);
+  }
+  return launch_status("prep_slices_kernel");
 }
 
 }  // namespace btfhip

@@ -1,0 +1,251 @@
+// slice.h -- a 1024-value slice of a vector held by one wave64 in registers,
+// 16 consecutive values per lane (lane l holds values 16 l .. 16 l + 15), and
+// what the activation prep, the embedding lookup and the step program do to
+// it without LDS: the blockwise fast Walsh-Hadamard transform, the Q8_0 of
+// each 32-value block (one lane pair) and the canonical sum of squares of the
+// RMSNorm.
+//
+// The FWHT follows the CPU's stage order (ref/bonsai-decoder/src/cpu_ops.cpp:
+// 76-88: len = 1, 2, 4, ...; x[j] = a + b, x[j + len] = a - b), so it is
+// bit-exact: stages len = 1..8 pair values inside a lane, stages len = 16 ..
+// 512 pair lane l with lane l ^ (len / 16), exchanged by DPP within a row
+// (xor 1, 2 directly; xor 4 and 8 as two mirrors each) and by
+// v_permlane16_swap / v_permlane32_swap across rows.
+#pragma once
+#include "common.h"
+
+namespace btfhip {
+
+constexpr int kSliceVals = 1024;  // values per wave
+
+// Value of lane l ^ X within the 16-lane DPP row (X = 1, 2, 4, 8). A
+// composition dpp<B>(dpp<A>(v)) reads lane srcA(srcB(l)): row_half_mirror is
+// l ^ 7, row_mirror l ^ 15, quad_perm(3,2,1,0) l ^ 3.
+template <int X>
+__device__ __forceinline__ float lane_xor(float v) {
+  static_assert(X == 1 || X == 2 || X == 4 || X == 8, "DPP exchange within a row");
+  if constexpr (X == 1) return dpp_f<0xB1>(v);                // quad_perm(1,0,3,2)
+  if constexpr (X == 2) return dpp_f<0x4E>(v);                // quad_perm(2,3,0,1)
+  if constexpr (X == 4) return dpp_f<0x1B>(dpp_f<0x141>(v));  // (l ^ 3) ^ 7
+  return dpp_f<0x141>(dpp_f<0x140>(v));                       // (l ^ 7) ^ 15
+}
+template <int X>
+__device__ __forceinline__ int lane_xor_i(int v) {
+  return __float_as_int(lane_xor<X>(__int_as_float(v)));
+}
+template <int X>
+__device__ __forceinline__ double lane_xor_d(double v) {
+  const uint64_t u = __double_as_longlong(v);
+  const uint32_t lo = (uint32_t)__float_as_uint(lane_xor<X>(__uint_as_float((uint32_t)u)));
+  const uint32_t hi = (uint32_t)__float_as_uint(lane_xor<X>(__uint_as_float((uint32_t)(u >> 32))));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+// The values of the lane pair (l & ~16, l | 16) -- lo, hi -- in both lanes
+// (v_permlane16_swap of a register with itself), and of (l & ~32, l | 32).
+__device__ __forceinline__ void pair16(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+__device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
+// One cross-lane butterfly stage: the lower lane of each pair keeps a + b,
+// the upper a - b (a = the lower lane's value).
+template <int X>
+__device__ __forceinline__ void xstage(float (&v)[16], int lane) {
+  const bool upper = (lane & X) != 0;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    if constexpr (X <= 8) {
+      const float p = lane_xor<X>(v[i]);
+      v[i] = upper ? p - v[i] : v[i] + p;
+    } else {
+      float lo, hi;
+      if constexpr (X == 16)
+        pair16(v[i], lo, hi);
+      else
+        pair32(v[i], lo, hi);
+      v[i] = upper ? lo - hi : lo + hi;
+    }
+  }
+}
+
+// Blockwise FWHT butterflies (no scaling) of the wave's slice: every
+// `block`-sized run of consecutive values (block a power of two, 1..1024;
+// block <= 1 is no transform). Uniform control flow: `block` is the same in
+// every lane.
+template <int LEN>
+__device__ __forceinline__ void istage(float (&v)[16]) {  // an in-lane stage
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j & LEN) continue;
+    const float a = v[j], b = v[j + LEN];
+    v[j] = a + b;
+    v[j + LEN] = a - b;
+  }
+}
+__device__ __forceinline__ void slice_fwht(float (&v)[16], int lane, int block) {
+  if (block > 1) istage<1>(v);
+  if (block > 2) istage<2>(v);
+  if (block > 4) istage<4>(v);
+  if (block > 8) istage<8>(v);
+  if (block > 16) xstage<1>(v, lane);
+  if (block > 32) xstage<2>(v, lane);
+  if (block > 64) xstage<4>(v, lane);
+  if (block > 128) xstage<8>(v, lane);
+  if (block > 256) xstage<16>(v, lane);
+  if (block > 512) xstage<32>(v, lane);
+}
+
+// Q8_0 of the 32-value block held by a lane pair (l, l ^ 1): the q bytes of
+// this lane's 16 values as 4 little-endian words (word k = values 4k..4k+3),
+// and the block's d and s in both lanes. Arithmetic of the q8 kernel
+// (include/btf/packed.hpp:117-134): d = fp16_rn(amax / 127) widened, an
+// all-zero block's d carries the sign of its last value (the CPU's running
+// amax keeps the last zero it compared), q = rint(x * (127 / amax)), s = sum q.
+__device__ __forceinline__ void q8_pair(const float (&v)[16], int lane, uint32_t (&qw)[4], float& d, int& s) {
+  float amax = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  amax = fmaxf(amax, lane_xor<1>(amax));
+  const float other15 = lane_xor<1>(v[15]);
+  const float last = (lane & 1) ? v[15] : other15;  // value 31 of the block
+  float dd = h2f(f2h_bits(amax / 127.0f));
+  if (amax == 0.f) dd = copysignf(0.f, last);
+  const float id = amax != 0.f ? 127.0f / amax : 0.f;
+  int sum = 0;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    uint32_t w = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int q = (int)__builtin_rintf(v[4 * k + b] * id);
+      sum += q;
+      w |= (uint32_t)(q & 0xff) << (8 * b);
+    }
+    qw[k] = w;
+  }
+  s = sum + lane_xor_i<1>(sum);
+  d = dd;
+}
+
+// Canonical sum of squares of a 32-value block, in double: the pairwise tree
+// over the value index bits 0, 1, 2, 3, 4 (squares of floats are exact in
+// double). Here the lane pair holds the block (levels 1-4 in the lane, level
+// 5 across the pair); the step program's producers compute the same tree with
+// one value per lane. Both lanes get the sum.
+__device__ __forceinline__ double pair_sumsq(const float (&v)[16]) {
+  double t[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const double a = (double)v[2 * i], b = (double)v[2 * i + 1];
+    const double sa = a * a, sb = b * b;
+    t[i] = sa + sb;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) t[i] = t[2 * i] + t[2 * i + 1];
+  t[0] = t[0] + t[1];
+  t[1] = t[2] + t[3];
+  t[0] = t[0] + t[1];
+  return t[0] + lane_xor_d<1>(t[0]);
+}
+
+// Sum over the wave of one double per lane, every lane getting the total:
+// a butterfly over lane bits 0..5 (each pair adds the same two values, so all
+// lanes agree bit for bit).
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v += lane_xor_d<1>(v);
+  v += lane_xor_d<2>(v);
+  v += lane_xor_d<4>(v);
+  v += lane_xor_d<8>(v);
+  {
+    const uint64_t u = __double_as_longlong(v);
+    float llo, lhi, hlo, hhi;
+    pair16(__uint_as_float((uint32_t)u), llo, lhi);
+    pair16(__uint_as_float((uint32_t)(u >> 32)), hlo, hhi);
+    const double a = __longlong_as_double((long long)(((uint64_t)__float_as_uint(hlo) << 32) | __float_as_uint(llo)));
+    const double b = __longlong_as_double((long long)(((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi)));
+    v = a + b;
+  }
+  {
+    const uint64_t u = __double_as_longlong(v);
+    float llo, lhi, hlo, hhi;
+    pair32(__uint_as_float((uint32_t)u), llo, lhi);
+    pair32(__uint_as_float((uint32_t)(u >> 32)), hlo, hhi);
+    const double a = __longlong_as_double((long long)(((uint64_t)__float_as_uint(hlo) << 32) | __float_as_uint(llo)));
+    const double b = __longlong_as_double((long long)(((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi)));
+    v = a + b;
+  }
+  return v;
+}
+
+// The RMSNorm scale from the canonical total of the row's block sums:
+// lane l adds block sums l, l + 64, ... in order (from 0), then wave_sum_d;
+// mean = f32(total / n), scale = 1 / sqrtf(mean + eps)
+// (ref/bonsai-decoder/src/cpu_ops.cpp:121-127). `get(i)` returns block sum i.
+template <class Get>
+__device__ __forceinline__ float norm_scale(Get get, int nblocks, int n, float eps, int lane) {
+  double acc = 0.0;
+  for (int i = lane; i < nblocks; i += 64) acc += get(i);
+  const double total = wave_sum_d(acc);
+  const float mean = (float)(total / (double)n);
+  return 1.0f / sqrtf(mean + eps);
+}
+
+// ---- greedy-pick keys ----
+// A total order on (value, index) as one 64-bit key: the value's bits made
+// order-preserving in the high word (negative: all bits flipped; otherwise
+// the sign bit set; -0 is first folded onto +0, as -0 == +0), the complement
+// of the index in the low word (the smaller index wins a tie). A NaN gets key
+// 0, below every number's key (-inf maps to 0x007FFFFF...), so it never wins
+// and an all-NaN input keeps key 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, int i) {
+  if (v != v) return 0;
+  const uint32_t b = __float_as_uint(v + 0.0f);
+  const uint32_t o = (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+  return ((uint64_t)o << 32) | (uint32_t)~(uint32_t)i;
+}
+__device__ __forceinline__ uint64_t key_max(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ int argmax_key_index(uint64_t k) { return k ? (int)~(uint32_t)k : 0; }
+// Max over the wave's 64 keys, in every lane.
+__device__ __forceinline__ uint64_t wave_max_key(uint64_t k) {
+  auto xchg = [](uint64_t v, auto f) {
+    const uint32_t lo = __float_as_uint(f(__uint_as_float((uint32_t)v)));
+    const uint32_t hi = __float_as_uint(f(__uint_as_float((uint32_t)(v >> 32))));
+    return ((uint64_t)hi << 32) | lo;
+  };
+  k = key_max(k, xchg(k, [](float x) { return lane_xor<1>(x); }));
+  k = key_max(k, xchg(k, [](float x) { return lane_xor<2>(x); }));
+  k = key_max(k, xchg(k, [](float x) { return lane_xor<4>(x); }));
+  k = key_max(k, xchg(k, [](float x) { return lane_xor<8>(x); }));
+  {
+    float llo, lhi, hlo, hhi;
+    pair16(__uint_as_float((uint32_t)k), llo, lhi);
+    pair16(__uint_as_float((uint32_t)(k >> 32)), hlo, hhi);
+    k = key_max(((uint64_t)__float_as_uint(hlo) << 32) | __float_as_uint(llo),
+                ((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi));
+  }
+  {
+    float llo, lhi, hlo, hhi;
+    pair32(__uint_as_float((uint32_t)k), llo, lhi);
+    pair32(__uint_as_float((uint32_t)(k >> 32)), hlo, hhi);
+    k = key_max(((uint64_t)__float_as_uint(hlo) << 32) | __float_as_uint(llo),
+                ((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi));
+  }
+  return k;
+}
+
+// Source index of destination og under the tiled -> grouped gather
+// (ref/bonsai-decoder/src/cpu_ops.cpp:96-104: out[d + hd (r + rep k)] =
+// x[d + hd (k + nk r)]).
+__device__ __forceinline__ int perm_src(int og, int hd, int nk, int rep) {
+  const int dd = og % hd, t = og / hd;
+  const int r = t % rep, k = t / rep;
+  return dd + hd * (k + nk * r);
+}
+
+}  // namespace btfhip

@@ -117,7 +117,9 @@ def test_invalid_arguments_rejected_on_host():
     assert h.launch_embed_raw(codes + 2, scales, tok, 1, 1024, None, y) == ARGS             # codes alignment
     assert h.launch_embed_raw(codes, scales, tok, 1, 1024, h.Hx(block=96), y) == ARGS       # block not 2^k
     assert h.launch_embed_raw(codes, scales, tok, 0, 1024, None, y) == h.BTF_OK            # M = 0: no-op
-    assert h.argmax_part_bytes(248320) >= 128 * 8
+    # one 8-byte key per part of up to 2048 logits, at most 256 parts
+    assert h.argmax_part_bytes(248320) == 8 * ((248320 + 2047) // 2048)
+    assert h.argmax_part_bytes(10 ** 7) == 8 * 256 and h.argmax_part_bytes(1) == 8
     assert h.launch_argmax_raw(y, 0, y, tok) == ARGS                                        # empty vocabulary
     assert h.launch_argmax_raw(y, 100, y + 4, tok) == ARGS                                  # part alignment
     assert h.launch_argmax_raw(None, 100, y, tok) == ARGS                                   # null logits

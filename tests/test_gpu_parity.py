@@ -167,7 +167,13 @@ def test_q8_unaligned_rows(hip, oracle):
 # (n, hadamard block, norm, perm, signs, M)
 PREP_CASES = [(1024, 64, True, False, True, 1), (5120, 1024, True, False, True, 3),
               (2048, 128, False, True, True, 8), (256, 0, True, False, False, 2),
-              (17408, 1024, False, False, True, 1)]
+              (17408, 1024, False, False, True, 1),
+              # beyond the reference's cases: a tail slice (1056 = 1024 + 32, span 32),
+              # blocks below one lane's 16 values, 17 slices with the norm (more
+              # slices than waves), the perm under the norm, a 3-slice row
+              (1056, 32, True, False, True, 2), (1056, 16, False, False, False, 3), (2048, 2, True, False, True, 1),
+              (17408, 1024, True, False, True, 2), (4096, 512, True, True, False, 5), (3072, 1024, False, False, True, 4),
+              (5120, 1, True, False, True, 1), (96, 32, False, False, True, 1)]
 
 
 @pytest.mark.parametrize("n,block,norm,perm,signs,M", PREP_CASES)
@@ -186,6 +192,7 @@ def test_prep_full(hip, oracle, n, block, norm, perm, signs, M):
     hx = hip.Hx(block, hd, nk, rep, dev(sg) if signs else None)
     hip.launch_prep(dev(x), n, M, n, dev(w) if norm else None, eps, hx, xn, n, a, stream())
     gq, gd, gs, gxn = host(a.q), host(a.d), host(a.s), host(xn)
+    assert np.isfinite(gd).all()
     # The reference's bars (tests/test_gpu_kernels.cpp:152-158). Without the
     # norm every stage is order-identical, so the result is bit-exact.
     dq = np.abs(gq.astype(np.int32) - q_ref.astype(np.int32))
@@ -197,6 +204,37 @@ def test_prep_full(hip, oracle, n, block, norm, perm, signs, M):
         assert np.array_equal(gd.view(np.uint32), d_ref.view(np.uint32))
         assert np.array_equal(gs, s_ref)
         assert np.array_equal(gxn, xn_ref)
+
+
+def test_prep_zero_rows_and_blocks(hip, oracle):
+    """All-zero rows (norm scale 1/sqrt(eps)) and zero blocks (d = +-0 with
+    the sign of the block's last value) through the full prep, bit-exact
+    without the norm, within the reference's bars with it."""
+    rng = np.random.default_rng(99)
+    n, M = 2048, 3
+    x = (rng.standard_normal((M, n)) * 2).astype(np.float32)
+    x[0] = 0.0
+    x[1, 64:96] = 0.0
+    x[1, 127] = -0.0
+    x[2, 1024:1056] = -0.0
+    w = rng.standard_normal(n).astype(np.float32)
+    sg = np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float32)
+    torch = _torch()
+    for norm, block in ((False, 0), (False, 64), (True, 256)):
+        q_ref, d_ref, s_ref, _ = oracle.prep(x, w if norm else None, 1e-6, block, 0, 0, 0, sg if block else None)
+        a = hip.Q8Act(zeros((M, n), torch.int8), zeros((M, n // 32), torch.float32), zeros((M, n // 32), torch.int32))
+        xn = zeros((M, n), torch.float32)  # forces the full prep kernel even without norm and transform
+        hip.launch_prep(dev(x), n, M, n, dev(w) if norm else None, 1e-6, hip.Hx(block, 0, 0, 0, dev(sg) if block else None),
+                        xn, n, a, stream())
+        gq, gd, gs = host(a.q), host(a.d), host(a.s)
+        if norm:
+            dq = np.abs(gq.astype(np.int32) - q_ref.astype(np.int32))
+            assert dq.max() <= 1 and (dq != 0).mean() <= 1e-3
+            assert rel_rms(gd, d_ref) <= 1e-4
+        else:
+            assert np.array_equal(gq, q_ref)
+            assert np.array_equal(gd.view(np.uint32), d_ref.view(np.uint32)), f"block {block}: d bits"
+            assert np.array_equal(gs, s_ref)
 
 
 # ---------------------------------------------------------------- GEMV / GEMM
@@ -613,7 +651,9 @@ def test_gemv_fused_chain_matches_prep_chain(hip, oracle):
 
 
 @pytest.mark.parametrize("E,block,mapped", [(1024, 0, False), (5120, 1024, False), (5120, 128, True),
-                                             (2048, 1024, False), (17408, 256, False)])
+                                             (2048, 1024, False), (17408, 256, False),
+                                             (1152, 128, False), (1152, 16, True), (3072, 1024, False),
+                                             (5120, 2, False), (128, 128, False)])
 def test_embed_bit_exact(hip, oracle, E, block, mapped):
     """Embedding rows of a packed table (device or mapped host memory) with
     the inverse transform equal the emulator's lookup (oracle) bit for bit;
@@ -657,7 +697,7 @@ def test_embed_block_wider_than_the_span_is_rejected(hip, oracle):
                          stream())
 
 
-@pytest.mark.parametrize("V", [1, 100, 4097, 248320])
+@pytest.mark.parametrize("V", [1, 100, 4097, 248320, 2048 * 256 + 77])
 def test_argmax_matches_oracle(hip, oracle, V):
     """Greedy pick over the logits: random values, a planted tie (the smaller
     index wins), all -inf but two, an interior NaN (never wins), all equal."""
@@ -677,6 +717,11 @@ def test_argmax_matches_oracle(hip, oracle, V):
         t[V // 2] = np.nan
         cases.append(t)
         cases.append(np.full(V, 0.5, np.float32))
+        t = np.full(V, -1.0, np.float32)
+        t[[3, V - 3]] = -0.0  # -0 == +0: the first one wins
+        t[V // 2] = 0.0
+        cases.append(t)
+        cases.append(np.full(V, np.nan, np.float32))
     for l in cases:
         hip.launch_argmax(dev(l), V, part, out, stream())
         assert int(host(out)[0]) == oracle.argmax(l)
