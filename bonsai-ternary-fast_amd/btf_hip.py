@@ -54,6 +54,12 @@ class _StepGemv(C.Structure):
                 ("up_codes", C.c_void_p), ("up_scales", C.c_void_p), ("in_vec", C.c_int), ("out_vec", C.c_int)]
 
 
+class _StepOp(C.Structure):
+    _fields_ = [("kind", C.c_int), ("gemv", _StepGemv), ("normw", C.c_void_p), ("eps", C.c_float), ("hx", _Hx),
+                ("vec", C.c_int), ("table_codes", C.c_void_p), ("table_scales", C.c_void_p), ("d_tok", C.c_void_p),
+                ("d_tok_out", C.c_void_p), ("d_pos", C.c_void_p)]
+
+
 class _DeviceInfo(C.Structure):
     _fields_ = [("cu_count", C.c_int), ("lds_bytes_per_block", C.c_int), ("max_clock_khz", C.c_int),
                 ("mem_clock_khz", C.c_int), ("mem_bus_width_bits", C.c_int), ("l2_bytes", C.c_int),
@@ -121,6 +127,8 @@ _host_alloc_mapped = _decl("btf_hip_host_alloc_mapped", [C.POINTER(C.c_void_p), 
 _host_free = _decl("btf_hip_host_free", [_vp])
 _step_create = _decl("btf_hip_step_create",
                      [C.POINTER(_StepVec), _i, C.POINTER(_StepGemv), _i, C.POINTER(C.c_void_p)])
+_step_create_ops = _decl("btf_hip_step_create_ops",
+                         [C.POINTER(_StepVec), _i, C.POINTER(_StepOp), _i, C.POINTER(C.c_void_p)])
 _step_launch = _decl("btf_hip_step_launch", [_vp, _vp])
 _step_error = _decl("btf_hip_step_error", [_vp, C.POINTER(C.c_int)])
 _step_destroy = _decl("btf_hip_step_destroy", [_vp])
@@ -152,7 +160,8 @@ ABI_SYMBOLS = (
     "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
     "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
     "btf_hip_graph_destroy", "btf_hip_step_create", "btf_hip_step_launch", "btf_hip_step_error",
-    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_gguf_open", "btf_hip_gguf_close",
+    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_step_create_ops", "btf_hip_gguf_open",
+    "btf_hip_gguf_close",
     "btf_hip_gguf_info", "btf_hip_gguf_tensor", "btf_hip_gguf_find_tensor", "btf_hip_gguf_kv",
     "btf_hip_gguf_find_kv", "btf_hip_gguf_kv_num", "btf_hip_gguf_kv_str", "btf_hip_ggml_row_bytes",
     "btf_hip_gguf_plan", "btf_hip_loader_create", "btf_hip_loader_upload_ptq1_0", "btf_hip_loader_finish",
@@ -366,7 +375,9 @@ class StepVec:
 
 @dataclass
 class StepGemv:
-    """One GEMV of a step program (swiglu: codes/scales = gate, up_* = up)."""
+    """One GEMV of a step program (swiglu: codes/scales = gate, up_* = up).
+    normw / eps / hx: the input's prep (launch_prep's RMSNorm and transform),
+    for whole-token programs."""
     mode: int
     K: int
     N: int
@@ -376,6 +387,62 @@ class StepGemv:
     out_vec: int
     up_codes: object = None
     up_scales: object = None
+    normw: object = None
+    eps: float = 0.0
+    hx: "Hx" = None
+
+    def has_prep(self) -> bool:
+        return self.normw is not None or (self.hx is not None and self.hx.block > 0)
+
+
+@dataclass
+class StepEmbed:
+    """Embedding lookup of a whole-token program: vector `vec` = row *d_tok
+    of the packed table, with the inverse transform `inv`."""
+    vec: int
+    table_codes: object
+    table_scales: object
+    d_tok: object
+    inv: "Hx" = None
+
+
+@dataclass
+class StepArgmax:
+    """Greedy pick over vector `vec` (directly after the GEMV that writes it)
+    into *d_tok_out, then *d_pos += 1 if d_pos is given."""
+    vec: int
+    d_tok_out: object
+    d_pos: object = None
+
+
+STEP_GEMV, STEP_EMBED, STEP_ARGMAX = 0, 1, 2
+
+
+def _step_gemv_c(g):
+    return _StepGemv(int(g.mode), g.K, g.N, _addr(g.codes), _addr(g.scales), _addr(g.up_codes), _addr(g.up_scales),
+                     g.in_vec, g.out_vec)
+
+
+def _step_op_c(o):
+    c = _StepOp()
+    if isinstance(o, StepGemv):
+        c.kind = STEP_GEMV
+        c.gemv = _step_gemv_c(o)
+        c.normw = _addr(o.normw)
+        c.eps = o.eps
+        c.hx = (o.hx or Hx())._c()
+    elif isinstance(o, StepEmbed):
+        c.kind = STEP_EMBED
+        c.vec = o.vec
+        c.table_codes, c.table_scales, c.d_tok = _addr(o.table_codes), _addr(o.table_scales), _addr(o.d_tok)
+        c.hx = (o.inv or Hx())._c()
+    elif isinstance(o, StepArgmax):
+        c.kind = STEP_ARGMAX
+        c.vec = o.vec
+        c.d_tok_out, c.d_pos = _addr(o.d_tok_out), _addr(o.d_pos)
+    else:
+        c.kind = int(o)  # a raw kind (argument-check tests)
+    return c
 
 
 class StepProgram:
@@ -383,15 +450,19 @@ class StepProgram:
     (btf_hip_step_create / _launch / _error / _destroy). The vectors' data
     tensors must stay alive while the program exists."""
 
-    def __init__(self, vecs, gemvs):
+    def __init__(self, vecs, ops):
+        """ops: StepGemv only (btf_hip_step_create), or with StepEmbed /
+        StepArgmax / GEMV preps (btf_hip_step_create_ops)."""
         cv = (_StepVec * len(vecs))(*[_StepVec(v.n, _addr(v.data)) for v in vecs])
-        cg = (_StepGemv * len(gemvs))(*[
-            _StepGemv(int(g.mode), g.K, g.N, _addr(g.codes), _addr(g.scales), _addr(g.up_codes), _addr(g.up_scales),
-                      g.in_vec, g.out_vec) for g in gemvs])
         h = C.c_void_p()
-        _check(_step_create(cv, len(vecs), cg, len(gemvs), C.byref(h)))
+        if all(isinstance(o, StepGemv) and not o.has_prep() for o in ops):
+            cg = (_StepGemv * len(ops))(*[_step_gemv_c(g) for g in ops])
+            _check(_step_create(cv, len(vecs), cg, len(ops), C.byref(h)))
+        else:
+            co = (_StepOp * len(ops))(*[_step_op_c(o) for o in ops])
+            _check(_step_create_ops(cv, len(vecs), co, len(ops), C.byref(h)))
         self.h = h.value
-        self._keep = (vecs, gemvs)
+        self._keep = (vecs, ops)
 
     def launch(self, stream=None):
         _check(_step_launch(self.h, _stream(stream)))
@@ -416,6 +487,17 @@ class StepProgram:
 
     def __del__(self):
         _finalize(self)
+
+
+def step_create_ops_raw(vecs, ops) -> int:
+    """Status code of btf_hip_step_create_ops (the program is destroyed at once)."""
+    cv = (_StepVec * max(1, len(vecs)))(*[_StepVec(v.n, _addr(v.data)) for v in vecs])
+    co = (_StepOp * max(1, len(ops)))(*[_step_op_c(o) for o in ops])
+    h = C.c_void_p()
+    rc = _step_create_ops(cv, len(vecs), co, len(ops), C.byref(h))
+    if rc == BTF_OK:
+        _step_destroy(h.value)
+    return rc
 
 
 def step_create_raw(vecs, gemvs) -> int:

@@ -316,6 +316,17 @@ int btf_hip_step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv*
   return rc;
 }
 
+int btf_hip_step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, btf_step_t* out) {
+  if (!vecs || !ops || !out || nvec <= 0 || nops <= 0) return fail(BTF_ERR_ARGS, "step: empty program");
+  if (const int rc = step_validate_ops(vecs, nvec, ops, nops)) return rc;
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  StepProgram* P = nullptr;
+  const int rc = step_create_ops(vecs, nvec, ops, nops, &P, *ds);
+  if (rc == BTF_OK) *out = P;
+  return rc;
+}
+
 int btf_hip_step_launch(btf_step_t prog, btf_stream_t stream) {
   if (!prog) return fail(BTF_ERR_ARGS, "step: null program");
   return step_launch(static_cast<StepProgram*>(prog), static_cast<hipStream_t>(stream));

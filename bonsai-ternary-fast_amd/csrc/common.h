@@ -175,6 +175,9 @@ struct StepProgram;
 int step_validate(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops);  // host only
 int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops, StepProgram** out,
                 const DevState& ds);
+int step_validate_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops);  // host only
+int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, StepProgram** out,
+                    const DevState& ds);
 int step_check_residency(const DevState& ds);
 int step_launch(StepProgram* P, hipStream_t st);
 int step_error(StepProgram* P, int* err);

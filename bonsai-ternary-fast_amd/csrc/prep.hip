@@ -143,7 +143,9 @@ __global__ void __launch_bounds__(1024) prep_slices_kernel(PrepArgs a) {
       if (!(lane & 1) && c0 < a.n) bsum[c0 >> 5] = bs;
     }
     __syncthreads();
-    scale = norm_scale([&](int i) { return bsum[i]; }, a.n >> 5, a.n, a.eps, lane);
+    double acc = 0.0;
+    for (int i = lane; i < (a.n >> 5); i += 64) acc += bsum[i];
+    scale = norm_scale_of(acc, a.n, a.eps);
   }
   const bool xform = a.block > 0;
   for (int sl = wave; sl < a.nslices; sl += W) {
@@ -178,7 +180,7 @@ __global__ void __launch_bounds__(1024) prep_slices_kernel(PrepArgs a) {
     uint32_t qw[4];
     float dd;
     int ss;
-    q8_pair(v, lane, qw, dd, ss);
+    q8_pair(v, qw, dd, ss);
     if (live) {
       uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + (size_t)m * a.n + c0);
       qp[0] = qw[0];

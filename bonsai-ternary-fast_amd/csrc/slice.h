@@ -54,22 +54,26 @@ __device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
 }
 
 // One cross-lane butterfly stage: the lower lane of each pair keeps a + b,
-// the upper a - b (a = the lower lane's value).
+// the upper a - b (a = the lower lane's value, b the upper's). Without a
+// lane select: each lane adds its partner's value to its own with the sign
+// bit flipped in the upper lane, p + (-v) == p - v exactly in IEEE (so no
+// lane mask is held in scalar registers through the kernel).
 template <int X>
 __device__ __forceinline__ void xstage(float (&v)[16], int lane) {
-  const bool upper = (lane & X) != 0;
+  constexpr int kBit = X == 1 ? 0 : X == 2 ? 1 : X == 4 ? 2 : X == 8 ? 3 : X == 16 ? 4 : 5;
+  const uint32_t flip = ((uint32_t)lane >> kBit & 1u) << 31;  // the upper lane negates its own value
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
     if constexpr (X <= 8) {
       const float p = lane_xor<X>(v[i]);
-      v[i] = upper ? p - v[i] : v[i] + p;
+      v[i] = p + __uint_as_float(__float_as_uint(v[i]) ^ flip);
     } else {
       float lo, hi;
       if constexpr (X == 16)
         pair16(v[i], lo, hi);
       else
         pair32(v[i], lo, hi);
-      v[i] = upper ? lo - hi : lo + hi;
+      v[i] = lo + __uint_as_float(__float_as_uint(hi) ^ flip);
     }
   }
 }
@@ -89,6 +93,9 @@ __device__ __forceinline__ void istage(float (&v)[16]) {  // an in-lane stage
   }
 }
 __device__ __forceinline__ void slice_fwht(float (&v)[16], int lane, int block) {
+  // (`block` passes an empty asm: its comparisons are made here, per call,
+  // not hoisted out of a caller's loop into scalar registers held through it)
+  asm volatile("" : "+s"(block));
   if (block > 1) istage<1>(v);
   if (block > 2) istage<2>(v);
   if (block > 4) istage<4>(v);
@@ -107,13 +114,12 @@ __device__ __forceinline__ void slice_fwht(float (&v)[16], int lane, int block) 
 // (include/btf/packed.hpp:117-134): d = fp16_rn(amax / 127) widened, an
 // all-zero block's d carries the sign of its last value (the CPU's running
 // amax keeps the last zero it compared), q = rint(x * (127 / amax)), s = sum q.
-__device__ __forceinline__ void q8_pair(const float (&v)[16], int lane, uint32_t (&qw)[4], float& d, int& s) {
+__device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t (&qw)[4], float& d, int& s) {
   float amax = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
   amax = fmaxf(amax, lane_xor<1>(amax));
-  const float other15 = lane_xor<1>(v[15]);
-  const float last = (lane & 1) ? v[15] : other15;  // value 31 of the block
+  const float last = dpp_f<0xF5>(v[15]);  // quad_perm(1,1,3,3): the odd lane's v[15], value 31 of the block
   float dd = h2f(f2h_bits(amax / 127.0f));
   if (amax == 0.f) dd = copysignf(0.f, last);
   const float id = amax != 0.f ? 127.0f / amax : 0.f;
@@ -183,14 +189,11 @@ __device__ __forceinline__ double wave_sum_d(double v) {
   return v;
 }
 
-// The RMSNorm scale from the canonical total of the row's block sums:
-// lane l adds block sums l, l + 64, ... in order (from 0), then wave_sum_d;
-// mean = f32(total / n), scale = 1 / sqrtf(mean + eps)
-// (ref/bonsai-decoder/src/cpu_ops.cpp:121-127). `get(i)` returns block sum i.
-template <class Get>
-__device__ __forceinline__ float norm_scale(Get get, int nblocks, int n, float eps, int lane) {
-  double acc = 0.0;
-  for (int i = lane; i < nblocks; i += 64) acc += get(i);
+// The RMSNorm scale from the canonical total of a row's block sums of
+// squares: lane l adds block sums l, l + 64, ... in order, from 0 (acc);
+// then wave_sum_d; mean = f32(total / n), scale = 1 / sqrtf(mean + eps)
+// (ref/bonsai-decoder/src/cpu_ops.cpp:121-127).
+__device__ __forceinline__ float norm_scale_of(double acc, int n, float eps) {
   const double total = wave_sum_d(acc);
   const float mean = (float)(total / (double)n);
   return 1.0f / sqrtf(mean + eps);

@@ -41,11 +41,13 @@
 
 #include <algorithm>
 #include <climits>
+#include <cmath>
 #include <cstring>
 #include <vector>
 
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
+#include "slice.h"
 
 // Floating-point expressions are evaluated as written (no fused multiply-add
 // unless fmaf is spelled out), so the per-slice row sums have one defined
@@ -72,35 +74,62 @@ constexpr uint32_t kSpinMax = 1u << 20;     // poll bound (each poll is a memory
 
 // 144 bytes (a multiple of 16: copied into LDS in 16-byte words).
 struct OpDev {
-  int kind;  // 0 = quantize a user vector (prologue), 1 = GEMV
+  int kind;  // 0 = quantize a user vector (prologue), 1 = GEMV, 2 = embedding lookup (prologue)
   int mode;
   int K, N;
   int cpr;
-  int units, rot, qpu_log2;  // 32-row units, unit rotation, log2 row quads per unit (3; swiglu 4)
+  int units, rot, qpu_log2;  // units (32 rows; embedding: 1024 values), unit rotation, log2 row quads per unit
   int next;                  // index of the next GEMV op (nops: none)
-  int count_reads;           // 1: count the workgroups that have fetched this op's input
   int war_op;                // >= 0: wait until every workgroup has fetched that op's input
                              // (the last reader of the version this op overwrites)
+  int prep;                  // >= 0: index of the op's PrepDev (GEMV: its input's norm / transform,
+                             // read from the fp32 words; embedding: the inverse transform)
   uint32_t in_tag;           // relative tag of the input's producer
   uint32_t old_tag;          // add mode: relative tag of the output's previous version
   uint32_t my_tag;
-  uint8_t early;      // 1: the I/O waves fetch this op's input during the previous op
-  uint8_t carry_in;   // 1: add-mode old values come from the previous op's epilogue (LDS carry)
-  uint8_t carry_out;  // 1: the epilogue keeps its outputs in the LDS carry for the next op
-  uint8_t pad0;
-  int pad1;
-  const uint8_t* codes;
-  const uint16_t* scales;
+  uint8_t early;        // 1: the I/O waves fetch this op's input during the previous op
+  uint8_t carry_in;     // 1: add-mode old values come from the previous op's epilogue (LDS carry)
+  uint8_t carry_out;    // 1: the epilogue keeps its outputs in the LDS carry for the next op
+  uint8_t count_reads;  // 1: count the workgroups that have fetched this op's input
+  uint8_t out_sq;       // 1: also publish each 32-value block's sum of squares (a later op normalizes it)
+  uint8_t argmax;       // 1: the program's greedy pick reads this op's output
+  uint8_t pad0, pad1;
+  const uint8_t* codes;     // GEMV: weights (swiglu: gate); embedding: table codes
+  const uint16_t* scales;   // embedding: table scales
   const uint8_t* up_codes;
   const uint16_t* up_scales;
-  const uint64_t* in_q8;    // LL Q8 words of the input vector
+  const uint64_t* in_ll;    // LL words of the input: Q8 words, or with a prep its fp32 words
   float* out_plain;         // user output (nullable)
-  uint64_t* out_f32;        // LL fp32 of the output vector (nullable)
+  uint64_t* out_f32;        // LL fp32 of the output vector [N], then 2 LL words (low, high half of
+                            // a double) per 32-value block: the block sums of squares (nullable)
   uint64_t* out_q8;         // LL Q8 of the output vector (nullable)
   const uint64_t* old_f32;  // add mode: previous value of the output vector
-  const float* src;         // quantize op: user vector
+  const void* src;          // quantize: user vector (float); embedding: token id (int)
 };
 static_assert(sizeof(OpDev) == 144, "descriptor layout");
+
+// An op's activation prep (global memory, read with scalar loads once per op
+// per wave): launch_prep's pipeline for a GEMV input, or the inverse
+// transform of an embedding lookup (normw = NULL).
+struct PrepDev {
+  const float* normw;  // NULL: no RMSNorm
+  const float* signs;  // NULL: none
+  float eps;
+  float hs;            // 1 / sqrtf(block)
+  int block;           // 0: no transform
+  int hd, nk, rep;     // rep > 1: tiled -> grouped gather
+};
+
+// The program's greedy pick: every workgroup publishes the largest key of
+// the rows it produced of the picked vector (2 LL words: the key's low and
+// high halves) into parts[2 wg ..]; workgroup 0 reduces them at the end.
+struct HeadDev {
+  int present;
+  uint32_t tag;    // relative tag of the op that publishes the parts
+  int* tok_out;
+  int* pos;        // += 1 after the pick (nullable)
+  uint64_t* parts; // [G][2]
+};
 
 struct Ctl {
   uint32_t epoch;
@@ -146,6 +175,7 @@ struct Lds {
   float carry[kMaxOld];       // outputs of the workgroup's rows kept for the next (add-mode) op
   uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
   uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
+  uint64_t argk[kIW];         // per I/O wave: the largest pick key of the rows it published
   WorkRec wrec[kRecSlots][kCW];
   OpRec orec[kRecSlots];
   uint32_t epoch;
@@ -168,6 +198,14 @@ __device__ __forceinline__ void set_abort(Lds& L, Ctl* ctl) {
 }
 
 __device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
+// Is this lane 0 of its wave? Re-derived at each use (the empty asm hides
+// that the lane index never changes), so the compiler does not keep a lane
+// mask in scalar registers from the kernel's start.
+__device__ __forceinline__ bool first_lane(int lane) {
+  int t = lane & 63;
+  asm volatile("" : "+v"(t));
+  return t == 0;
+}
 template <class T>
 __device__ __forceinline__ T* sgpr_ptr(T* p) {
   const uint64_t u = reinterpret_cast<uint64_t>(p);
@@ -203,7 +241,7 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
 constexpr int kFB = 10;
 __device__ __forceinline__ void fetch_words(const OpDev& op, Lds& L, int lane, Ctl* ctl, uint32_t base_tag, int ob,
                                             int a0, int a1, int b0, int b1) {
-  const uint64_t* in = sgpr_ptr(op.in_q8);
+  const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int na = a1 - a0, nw = na + (b1 - b0);  // word k < nw: a0 + k, or b0 + k - na
   for (int k0 = 0; k0 < nw; k0 += kFB * 64) {
@@ -243,7 +281,7 @@ struct EarlyFetch {
   uint64_t v[kEIn];
 };
 __device__ __forceinline__ void early_issue(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f) {
-  const uint64_t* in = sgpr_ptr(op.in_q8);
+  const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
 #pragma unroll
@@ -257,7 +295,7 @@ __device__ __forceinline__ void early_issue(const OpDev& op, int lid, uint32_t b
 // false and some word of this wave is not yet published.
 __device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, Lds& L, int ob,
                                              Ctl* ctl, bool wait, uint32_t seq) {
-  const uint64_t* in = sgpr_ptr(op.in_q8);
+  const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int nin = (sgpr(op.K) / 32) * kWordsPerBlock;
   uint32_t spins = 0;
@@ -279,8 +317,133 @@ __device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t 
     if (idx < nin) L.act[ob][idx] = (uint32_t)f.v[b];
   }
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // the input words are in LDS
-  if ((lid & 63) == 0) __hip_atomic_store(&L.early_seq[lid >> 6], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  // (every lane of the wave stores the same value)
+  __hip_atomic_store(&L.early_seq[lid >> 6], seq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   return true;
+}
+
+// ---------------------------------------------------------------- prep input
+// With a prep (norm and/or transform), a GEMV reads its input's fp32 LL words
+// and runs launch_prep's pipeline itself: each compute wave, for every
+// 1024-value slice its items read, gathers the slice (through the perm),
+// normalizes it, applies the signs and the FWHT in registers (slice.h) and
+// writes the slice's Q8 into the LDS image, where the plain fetch would have
+// copied the producer's Q8 words. Bit-identical to launch_prep on the same
+// fp32 vector: the same per-slice arithmetic, and the RMSNorm scale from the
+// producers' block sums of squares summed in prep_slices_kernel's order.
+struct PrepRegs {  // a PrepDev in scalar registers
+  const float* normw;
+  const float* signs;
+  float eps, hs;
+  int block, hd, nk, rep;
+};
+__device__ __forceinline__ PrepRegs prep_regs(const PrepDev* preps, int i) {
+  const PrepDev& p = preps[i];
+  PrepRegs r;
+  r.normw = sgpr_ptr(p.normw);
+  r.signs = sgpr_ptr(p.signs);
+  r.eps = __int_as_float(sgpr(__float_as_int(p.eps)));
+  r.hs = __int_as_float(sgpr(__float_as_int(p.hs)));
+  r.block = sgpr(p.block);
+  r.hd = sgpr(p.hd);
+  r.nk = sgpr(p.nk);
+  r.rep = sgpr(p.rep);
+  return r;
+}
+
+constexpr int kSQ = 4;  // block sums of squares per lane per poll round
+// The RMSNorm scale of a GEMV's input: lane l adds the producers' block sums
+// l, l + 64, ... in order, then the wave sum (norm_scale_of).
+__device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd, Lds& L, int lane, Ctl* ctl,
+                                            uint32_t base_tag) {
+  const int K = sgpr(op.K), nb = K >> 5;
+  const uint64_t* sq = sgpr_ptr(op.in_ll) + K;
+  const uint32_t tin = base_tag + sgpr(op.in_tag);
+  double acc = 0.0;
+  for (int r0 = 0; r0 < nb; r0 += kSQ * 64) {
+    uint64_t lo[kSQ], hi[kSQ];
+#pragma unroll
+    for (int b = 0; b < kSQ; ++b) {
+      const int i = r0 + b * 64 + lane;
+      lo[b] = i < nb ? ll_load(sq + 2 * i) : ((uint64_t)tin << 32);
+      hi[b] = i < nb ? ll_load(sq + 2 * i + 1) : ((uint64_t)tin << 32);
+    }
+    uint32_t spins = 0;
+    for (;;) {
+      uint32_t pending = 0;
+#pragma unroll
+      for (int b = 0; b < kSQ; ++b)
+        pending |= ((uint32_t)(lo[b] >> 32) != tin || (uint32_t)(hi[b] >> 32) != tin) ? (1u << b) : 0u;
+      if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+      if (!poll_step(spins, L, ctl)) break;
+#pragma unroll
+      for (int b = 0; b < kSQ; ++b)
+        if (pending & (1u << b)) {
+          const int i = r0 + b * 64 + lane;
+          lo[b] = ll_load(sq + 2 * i);
+          hi[b] = ll_load(sq + 2 * i + 1);
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kSQ; ++b)
+      if (r0 + b * 64 + lane < nb)
+        acc += __longlong_as_double((long long)(((uint64_t)(uint32_t)hi[b] << 32) | (uint32_t)lo[b]));
+  }
+  return norm_scale_of(acc, K, pd.eps);
+}
+
+// Slice sl of a prep GEMV's input into LDS buffer `ob` (Q8 image).
+__device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepRegs& pd, float scale, Lds& L, int lane,
+                                                 Ctl* ctl, uint32_t base_tag, int ob, int sl) {
+  const uint64_t* in = sgpr_ptr(op.in_ll);
+  const uint32_t tin = base_tag + sgpr(op.in_tag);
+  const int c0 = sl * kSliceVals + 16 * lane;
+  // the lane's 16 values come from 16 consecutive sources (the step program
+  // takes perm_hd % 16 == 0, so a 16-value run never crosses a perm tile);
+  // the geometry passes an empty asm so its division constants are formed
+  // per slice, not held through the caller's loop
+  int hd = pd.hd, nk = pd.nk, rep = pd.rep;
+  asm volatile("" : "+s"(hd), "+s"(nk), "+s"(rep));
+  const int src0 = rep > 1 ? perm_src(c0, hd, nk, rep) : c0;
+  auto src = [&](int i) { return src0 + i; };
+  uint64_t w[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) w[i] = ll_load(in + src(i));
+  uint32_t spins = 0;
+  for (;;) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pending |= ((uint32_t)(w[i] >> 32) != tin) ? (1u << i) : 0u;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+    if (!poll_step(spins, L, ctl)) break;
+#pragma unroll
+    for (int i = 0; i < 16; ++i)
+      if (pending & (1u << i)) w[i] = ll_load(in + src(i));
+  }
+  float v[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) v[i] = __uint_as_float((uint32_t)w[i]);
+  if (pd.normw)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * pd.normw[src(i)];
+  if (pd.block > 0) {
+    if (pd.signs)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = v[i] * pd.signs[c0 + i];
+    slice_fwht(v, lane, pd.block);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * pd.hs;
+  }
+  uint32_t qw[4];
+  float d;
+  int s;
+  q8_pair(v, qw, d, s);
+  uint32_t* dst = &L.act[ob][(c0 >> 5) * kWordsPerBlock];
+  const int h = lane & 1;  // first or second half of the block's 8 q words
+#pragma unroll
+  for (int k = 0; k < 4; ++k) dst[4 * h + k] = qw[k];
+  dst[8] = __float_as_uint(d);  // both lanes of the pair store the block's d and s (the same values)
+  dst[9] = (uint32_t)s;
 }
 
 // ---------------------------------------------------------------- compute waves
@@ -363,6 +526,7 @@ __device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave,
 // Stage the records of op i (lanes 0 .. kCW-1 of the first I/O wave, one
 // per compute wave); read by the compute waves after the next barrier B.
 __device__ __forceinline__ void stage_work(Lds& L, int nops, int wg, int G, int i, int iol) {
+  asm volatile("" : "+v"(iol));  // lane tests formed here, not held from the kernel's start
   if (iol < kCW) {
     const OpWork w = op_work_calc(L, nops, iol, wg, G, i);
     const int slot = i % kRecSlots;
@@ -618,22 +782,27 @@ __device__ __forceinline__ bool sum_lanes(int l16) {
 // per-batch bookkeeping (addresses, partial-sum slots, the unit's count, the
 // activation reload at a new slice) is uniform and done once per batch.
 __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
-                                              uint32_t base_tag) {
+                                              uint32_t base_tag, const PrepDev* preps) {
   const int l16 = lane & 15, grp = lane >> 4;
   const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
   const bool sum_lane = sum_lanes(l16);
   const uint32_t hsh = (uint32_t)((l16 >> 1) & 1) * 16u;
   Slot ring[kRing];
-  OpWork cur = op_work(L, wave, first);
-  OpLd ld_cur = op_ld(L, first);
-  LaneOff lo_cur = lane_off(ld_cur, l16, grp);
   {
-    const BAddr a = batch_addr(ld_cur, cur.first, G, BPos{cur.u0, cur.s0, cur.q0});
+    const OpWork w0 = op_work(L, wave, first);
+    const OpLd d0 = op_ld(L, first);
+    const LaneOff l0 = lane_off(d0, l16, grp);
+    const BAddr a = batch_addr(d0, w0.first, G, BPos{w0.u0, w0.s0, w0.q0});
 #pragma unroll
-    for (int r = 0; r < kRing; ++r) issue_entry(ld_cur, lo_cur, a, r, ring[r]);
+    for (int r = 0; r < kRing; ++r) issue_entry(d0, l0, a, r, ring[r]);
   }
-  for (;;) {
-    const int ob = cur.i & 1;  // LDS buffers of this op
+  // Per op, the input fetch holds only the op index and the ring across it:
+  // the op's work record and load parameters are read again from LDS after
+  // it (the scalar registers they would hold are what the prep needs).
+  for (int opi = first;;) {
+    const int ob = opi & 1;  // LDS buffers of this op
+    {
+    const OpWork cur = op_work(L, wave, opi);
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
         // fetched by the I/O waves (early_seq only grows within a launch:
@@ -652,11 +821,26 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
       } else {
         int a0, a1, b0w, b1w;
         input_words(cur, a0, a1, b0w, b1w);
-        fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0w, b1w);
+        const int pi = sgpr(L.opd[cur.i].prep);
+        if (pi >= 0) {  // the input's prep, slice by slice (the ranges are whole slices)
+          const PrepRegs pd = prep_regs(preps, pi);
+          const float scale = pd.normw ? prep_scale(L.opd[cur.i], pd, L, lane, ctl, base_tag) : 1.0f;
+          constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
+          for (int sl = a0 / kWS; sl < a1 / kWS; ++sl)
+            fetch_prep_slice(L.opd[cur.i], pd, scale, L, lane, ctl, base_tag, ob, sl);
+          for (int sl = b0w / kWS; sl < b1w / kWS; ++sl)
+            fetch_prep_slice(L.opd[cur.i], pd, scale, L, lane, ctl, base_tag, ob, sl);
+        } else {
+          fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0w, b1w);
+        }
         // the words other lanes of this wave wrote are read below
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
     }
+    }
+    const OpWork cur = op_work(L, wave, opi);
+    OpLd ld_cur = op_ld(L, opi);
+    LaneOff lo_cur = lane_off(ld_cur, l16, grp);
     const int U = cur.S << cur.qlog;  // items per unit
     BPos cp{cur.u0, cur.s0, cur.q0};  // the batch being consumed
     uint32_t aq[16];
@@ -713,7 +897,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     }
     lds_barrier();  // B: every wave is done with the op
     if (cur.next >= nops) break;
-    cur = op_work(L, wave, cur.next);
+    opi = cur.next;
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the trailing dummy loads
 }
@@ -741,13 +925,105 @@ __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, f
     if (j == 0) ll_store(dst + 8, ((uint64_t)tag << 32) | __float_as_uint(d));
     if (j == 1) ll_store(dst + 9, ((uint64_t)tag << 32) | (uint32_t)s);
   }
+  if (sgpr(op.out_sq)) {
+    // the unit's sum of squares in the canonical tree over the value index
+    // bits 0..4 (= lane bits of the half-wave), as pair_sumsq
+    const double x = valid ? (double)v : 0.0;
+    double t = x * x;
+    t += lane_xor_d<1>(t);
+    t += lane_xor_d<2>(t);
+    t += lane_xor_d<4>(t);
+    t += lane_xor_d<8>(t);
+    float llo, lhi, hlo, hhi;  // rows 0 / 1 (2 / 3) of the half-wave
+    const uint64_t u = __double_as_longlong(t);
+    pair16(__uint_as_float((uint32_t)u), llo, lhi);
+    pair16(__uint_as_float((uint32_t)(u >> 32)), hlo, hhi);
+    t = __longlong_as_double((long long)(((uint64_t)__float_as_uint(hlo) << 32) | __float_as_uint(llo))) +
+        __longlong_as_double((long long)(((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi)));
+    if (j == 0) {
+      const uint64_t b = __double_as_longlong(t);
+      uint64_t* dst = out_f32 + sgpr(op.N) + 2 * unit;
+      ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)b);
+      ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(b >> 32));
+    }
+  }
+}
+
+// Publish a 1024-value slice held by one wave, 16 values per lane (an
+// embedding lookup's output): plain output, fp32 LL words, the block sums of
+// squares and the Q8 LL words (each lane pair one 32-value block).
+__device__ __forceinline__ void publish_slice(const OpDev& op, int c0, int lane, const float (&v)[16], uint32_t tag) {
+  float* out_plain = sgpr_ptr(op.out_plain);
+  uint64_t* out_f32 = sgpr_ptr(op.out_f32);
+  uint64_t* out_q8 = sgpr_ptr(op.out_q8);
+  if (out_plain) {
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(1))) f32x4 gf32x4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      ((gf32x4*)(out_plain + c0))[k] = f32x4{v[4 * k], v[4 * k + 1], v[4 * k + 2], v[4 * k + 3]};
+  }
+  if (out_f32) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) ll_store(out_f32 + c0 + i, ((uint64_t)tag << 32) | __float_as_uint(v[i]));
+  }
+  const int blk = c0 >> 5, h = lane & 1;
+  if (sgpr(op.out_sq)) {
+    const uint64_t b = __double_as_longlong(pair_sumsq(v));
+    if (!h) {
+      uint64_t* dst = out_f32 + sgpr(op.N) + 2 * blk;
+      ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)b);
+      ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(b >> 32));
+    }
+  }
+  if (out_q8) {
+    uint32_t qw[4];
+    float d;
+    int s;
+    q8_pair(v, qw, d, s);
+    uint64_t* dst = out_q8 + (size_t)blk * kWordsPerBlock;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) ll_store(dst + 4 * h + k, ((uint64_t)tag << 32) | qw[k]);
+    if (!h) {
+      ll_store(dst + 8, ((uint64_t)tag << 32) | __float_as_uint(d));
+      ll_store(dst + 9, ((uint64_t)tag << 32) | (uint32_t)s);
+    }
+  }
+}
+
+// The embedding lookup (an op of the prologue, by the I/O waves of the
+// workgroups that own its 1024-value units): as embed_slices_kernel, then
+// published like a GEMV output.
+__device__ __forceinline__ void io_embed(const OpDev& op, const PrepRegs& pd, int wg, int G, int iol, uint32_t tag) {
+  const int iw = iol >> 6, lane = iol & 63;
+  const int E = sgpr(op.N), units = sgpr(op.units);
+  const int tok = sgpr(*(const __attribute__((address_space(1))) int*)sgpr_ptr(static_cast<const int*>(op.src)));
+  const uint32_t* rowc = reinterpret_cast<const uint32_t*>(sgpr_ptr(op.codes) + (size_t)tok * (size_t)(E / 4));
+  const uint16_t* rows = sgpr_ptr(op.scales) + (size_t)tok * (size_t)(E / 128);
+  for (int u = first_unit(sgpr(op.rot), wg, G) + iw * G; u < units; u += kIW * G) {
+    const int c0 = u * kSliceVals + 16 * lane;
+    const uint32_t w = rowc[c0 >> 4];
+    const float sc = h2f(rows[c0 >> 7]);
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = (float)((int)((w >> (8 * (j & 3) + 2 * (j >> 2))) & 3u) - 1) * sc;
+    if (pd.block > 0) {
+      slice_fwht(v, lane, pd.block);
+#pragma unroll
+      for (int j = 0; j < 16; ++j) v[j] = v[j] * pd.hs;
+      if (pd.signs)
+#pragma unroll
+        for (int j = 0; j < 16; ++j) v[j] = v[j] * pd.signs[c0 + j];
+    }
+    publish_slice(op, c0, lane, v, tag);
+  }
 }
 
 __device__ __forceinline__ void io_quantize(const OpDev& op, int wg, int G, int iol, uint32_t tag) {
   // half-wave h of the I/O waves handles units first + (h + t*nhalves)*G
   const int half = iol >> 5, j = iol & 31, nhalves = kIW * 2;
   const int N = sgpr(op.N), units = sgpr(op.units);
-  const float* src = sgpr_ptr(op.src);
+  const float* src = sgpr_ptr(static_cast<const float*>(op.src));
   for (int u = first_unit(sgpr(op.rot), wg, G) + half * G; u < units; u += nhalves * G) {
     const int row = u * 32 + j;
     const bool valid = row < N;
@@ -798,6 +1074,8 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
     return (old_ll && ui < nunits && row < N) ? ll_load(old + row) : ((uint64_t)told << 32);
   };
   uint64_t ov = old_word(half);
+  const bool pick = sgpr(op.argmax);
+  uint64_t best = 0;  // the largest pick key of the rows this lane published
   for (int ui = half; ui < nunits; ui += nhalves) {
     {
       // polled at normal priority and sparsely: the compute waves on the
@@ -848,6 +1126,11 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
       if (carry_out) L.carry[lr] = v;
     }
     publish_unit(op, unit, j, valid ? v : 0.f, valid, tag);
+    if (pick && valid) best = key_max(best, argmax_key(v, row));
+  }
+  if (pick) {
+    best = wave_max_key(best);
+    L.argk[iol >> 6] = best;  // every lane stores the wave's key; combined after barrier B
   }
 }
 
@@ -855,12 +1138,63 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
 // input (if it is early), wait for the write-after-read guard, publish the
 // units as they complete, barrier B, count this workgroup's reads of the
 // op's input, finish the early fetch.
+// The program's greedy pick (workgroup 0's first I/O wave, after its last
+// op): the largest of the G workgroups' keys, polled from their LL words.
+__device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int lane, Ctl* ctl, uint32_t base_tag) {
+  const uint64_t* parts = sgpr_ptr(head->parts);
+  const uint32_t tag = base_tag + sgpr((int)head->tag);
+  constexpr int kPer = 4;  // parts per lane (G <= 256)
+  uint64_t lo[kPer], hi[kPer];
+#pragma unroll
+  for (int b = 0; b < kPer; ++b) {
+    const int w = lane + 64 * b;
+    lo[b] = w < G ? ll_load(parts + 2 * w) : ((uint64_t)tag << 32);
+    hi[b] = w < G ? ll_load(parts + 2 * w + 1) : ((uint64_t)tag << 32);
+  }
+  uint32_t spins = 0;
+  for (;;) {
+    uint32_t pending = 0;
+#pragma unroll
+    for (int b = 0; b < kPer; ++b)
+      pending |= ((uint32_t)(lo[b] >> 32) != tag || (uint32_t)(hi[b] >> 32) != tag) ? (1u << b) : 0u;
+    if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
+    if (!poll_step(spins, L, ctl)) break;
+#pragma unroll
+    for (int b = 0; b < kPer; ++b)
+      if (pending & (1u << b)) {
+        const int w = lane + 64 * b;
+        lo[b] = ll_load(parts + 2 * w);
+        hi[b] = ll_load(parts + 2 * w + 1);
+      }
+  }
+  uint64_t best = 0;
+#pragma unroll
+  for (int b = 0; b < kPer; ++b)
+    if (lane + 64 * b < G) best = key_max(best, ((uint64_t)(uint32_t)hi[b] << 32) | (uint32_t)lo[b]);
+  best = wave_max_key(best);
+  if (first_lane(lane)) {
+    *(__attribute__((address_space(1))) int*)sgpr_ptr(head->tok_out) = argmax_key_index(best);
+    int* pos = sgpr_ptr(head->pos);
+    if (pos) (void)__hip_atomic_fetch_add(pos, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The I/O waves' program. Per op: issue the early loads of the next op's
+// input (if it is early), wait for the write-after-read guard, publish the
+// units as they complete, barrier B, count this workgroup's reads of the
+// op's input (and publish its pick key), finish the early fetch. Prologue ops
+// (quantize, embedding) run before the first GEMV.
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
-                                         uint32_t base_tag) {
+                                         uint32_t base_tag, const PrepDev* preps, const HeadDev* head) {
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
-    if (sgpr(op.kind) == 0) {
+    const int kind = sgpr(op.kind);
+    if (kind == 0) {
       io_quantize(op, wg, G, iol, base_tag + sgpr(op.my_tag));
+      continue;
+    }
+    if (kind == 2) {
+      io_embed(op, prep_regs(preps, sgpr(op.prep)), wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
     const int nx = sgpr(op.next);
@@ -878,15 +1212,25 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     if (early) early_done = early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, false, (uint32_t)nx + 1);
     io_publish(op, L, wg, G, iol, base_tag, ctl);
     lds_barrier();  // B: every compute wave is done with the op's input
-    if (sgpr(op.count_reads) && iol == 0)
+    const bool io0 = sgpr(iol >> 6) == 0;  // the first I/O wave
+    if (sgpr(op.count_reads) && io0 && first_lane(iol))
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
+      const uint64_t k = key_max(L.argk[0], L.argk[1]);
+      uint64_t* dst = sgpr_ptr(head->parts) + 2 * wg;
+      const uint32_t tag = base_tag + sgpr(op.my_tag);
+      ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)k);
+      ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(k >> 32));
+    }
     if (!early_done) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, true, (uint32_t)nx + 1);
   }
+  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(head->present)) io_pick(head, L, G, iol, ctl, base_tag);
 }
 
 // ---------------------------------------------------------------- the kernel
 __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict__ ops, int nops, int first_gemv,
-                                                        Ctl* ctl, uint32_t* rd_cnt) {
+                                                        Ctl* ctl, uint32_t* rd_cnt, const PrepDev* __restrict__ preps,
+                                                        const HeadDev* __restrict__ head) {
   __shared__ Lds L;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wg = blockIdx.x, G = gridDim.x;
@@ -916,13 +1260,13 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
   const uint32_t base_tag = L.epoch * (uint32_t)(nops + 1);
 
   if (wave < kCW)
-    compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
+    compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag, preps);
   else {
     // The I/O waves' epilogue of an op is on the chain's critical path while
     // the compute waves already run the next op's dot products on the same
     // SIMDs: their instructions issue first (the waits in between sleep).
     __builtin_amdgcn_s_setprio(3);
-    io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
+    io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag, preps, head);
     __builtin_amdgcn_s_setprio(0);
   }
 
@@ -953,8 +1297,10 @@ struct StepProgram {
   int first = 0;  // index of the first GEMV op
   OpDev* d_ops = nullptr;
   Ctl* d_ctl = nullptr;
-  uint32_t* d_cnt = nullptr;  // per-op reader counters
-  std::vector<void*> bufs;    // every device buffer the program owns
+  uint32_t* d_cnt = nullptr;    // per-op reader counters
+  PrepDev* d_preps = nullptr;   // the ops' prep descriptors
+  HeadDev* d_head = nullptr;    // the greedy pick
+  std::vector<void*> bufs;      // every device buffer the program owns
 };
 
 void step_destroy(StepProgram* P) {
@@ -963,65 +1309,160 @@ void step_destroy(StepProgram* P) {
   delete P;
 }
 
-int step_validate(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, int ngemv) {
+namespace {
+bool pow2_upto(int b, int hi) { return b > 0 && b <= hi && (b & (b - 1)) == 0; }
+bool has_prep(const btf_step_op& o) { return o.normw != nullptr || o.hx.block > 0; }
+bool misaligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) != 0; }
+
+int check_gemv_op(const btf_step_vec* vecs, int nvec, const btf_step_op& o) {
+  const btf_step_gemv& g = o.gemv;
+  if (g.in_vec < 0 || g.in_vec >= nvec || g.out_vec < 0 || g.out_vec >= nvec)
+    return fail(BTF_ERR_ARGS, "step: vector index out of range");
+  if (g.mode != BTF_GEMV_STORE && g.mode != BTF_GEMV_ADD && g.mode != BTF_GEMV_SWIGLU)
+    return fail(BTF_ERR_ARGS, "step: unknown mode");
+  if (g.K <= 0 || g.K % 1024 || g.K > kMaxK) return fail(BTF_ERR_ARGS, "step: K must be a multiple of 1024, <= 20480");
+  if (g.N % 4) return fail(BTF_ERR_ARGS, "step: N must be a multiple of 4");
+  if ((uint64_t)g.N * (uint64_t)(g.K / 4) >= (1ull << 32)) return fail(BTF_ERR_ARGS, "step: a matrix must be below 4 GB");
+  if (g.K > vecs[g.in_vec].n) return fail(BTF_ERR_ARGS, "step: K exceeds the input vector");
+  if (g.N != vecs[g.out_vec].n) return fail(BTF_ERR_ARGS, "step: N must equal the output vector length");
+  if (g.in_vec == g.out_vec) return fail(BTF_ERR_ARGS, "step: a GEMV cannot read its own output vector");
+  if (!g.codes || !g.scales || (g.mode == BTF_GEMV_SWIGLU && (!g.up_codes || !g.up_scales)))
+    return fail(BTF_ERR_ARGS, "step: null weights");
+  if (misaligned(g.codes, 16) || (g.up_codes && misaligned(g.up_codes, 16)) || misaligned(g.scales, 2) ||
+      (g.up_scales && misaligned(g.up_scales, 2)))
+    return fail(BTF_ERR_ARGS, "step: codes must be 16-byte and scales 2-byte aligned");
+  if (has_prep(o)) {
+    if (vecs[g.in_vec].n != g.K) return fail(BTF_ERR_ARGS, "step: a GEMV with a norm or transform needs an input of length K");
+    if (o.hx.block < 0 || (o.hx.block > 0 && !pow2_upto(o.hx.block, 1024)))
+      return fail(BTF_ERR_ARGS, "step: hadamard block must be 0 or a power of two <= 1024");
+    if (o.hx.block > 0 && o.hx.perm_rep > 1 &&
+        (o.hx.perm_hd <= 0 || o.hx.perm_nk <= 0 || (int64_t)o.hx.perm_hd * o.hx.perm_nk * o.hx.perm_rep != g.K))
+      return fail(BTF_ERR_ARGS, "step: hadamard perm geometry");
+    if (o.hx.block > 0 && o.hx.perm_rep > 1 && o.hx.perm_hd % 16)
+      return fail(BTF_ERR_ARGS, "step: the perm's tile (perm_hd) must be a multiple of 16");
+  } else if (o.hx.block < 0) {
+    return fail(BTF_ERR_ARGS, "step: hadamard block must be 0 or a power of two <= 1024");
+  }
+  if (vecs[g.in_vec].n % 32) return fail(BTF_ERR_ARGS, "step: quantized vectors need n % 32 == 0");
+  return BTF_OK;
+}
+}  // namespace
+
+int step_validate_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops) {
   for (int v = 0; v < nvec; ++v)
     if (vecs[v].n <= 0) return fail(BTF_ERR_ARGS, "step: vector length must be positive");
-  for (int i = 0; i < ngemv; ++i) {
-    const btf_step_gemv& g = gemvs[i];
-    if (g.in_vec < 0 || g.in_vec >= nvec || g.out_vec < 0 || g.out_vec >= nvec)
-      return fail(BTF_ERR_ARGS, "step: vector index out of range");
-    if (g.mode != BTF_GEMV_STORE && g.mode != BTF_GEMV_ADD && g.mode != BTF_GEMV_SWIGLU)
-      return fail(BTF_ERR_ARGS, "step: unknown mode");
-    if (g.K <= 0 || g.K % 1024 || g.K > kMaxK)
-      return fail(BTF_ERR_ARGS, "step: K must be a multiple of 1024, <= 20480");
-    if (g.N % 4) return fail(BTF_ERR_ARGS, "step: N must be a multiple of 4");
-    if ((uint64_t)g.N * (uint64_t)(g.K / 4) >= (1ull << 32)) return fail(BTF_ERR_ARGS, "step: a matrix must be below 4 GB");
-    if (g.K > vecs[g.in_vec].n) return fail(BTF_ERR_ARGS, "step: K exceeds the input vector");
-    if (g.N != vecs[g.out_vec].n) return fail(BTF_ERR_ARGS, "step: N must equal the output vector length");
-    if (g.in_vec == g.out_vec) return fail(BTF_ERR_ARGS, "step: a GEMV cannot read its own output vector");
-    if (!g.codes || !g.scales || (g.mode == BTF_GEMV_SWIGLU && (!g.up_codes || !g.up_scales)))
-      return fail(BTF_ERR_ARGS, "step: null weights");
-    if ((reinterpret_cast<uintptr_t>(g.codes) & 15) || (g.up_codes && (reinterpret_cast<uintptr_t>(g.up_codes) & 15)) ||
-        (reinterpret_cast<uintptr_t>(g.scales) & 1) || (g.up_scales && (reinterpret_cast<uintptr_t>(g.up_scales) & 1)))
-      return fail(BTF_ERR_ARGS, "step: codes must be 16-byte and scales 2-byte aligned");
-  }
-  {
-    std::vector<int> writes(nvec, 0);
-    for (int i = 0; i < ngemv; ++i) {
-      const btf_step_gemv& g = gemvs[i];
+  std::vector<int> writes(nvec, 0);
+  bool seen_gemv = false;
+  int picks = 0;
+  for (int i = 0; i < nops; ++i) {
+    const btf_step_op& o = ops[i];
+    if (o.kind == BTF_STEP_EMBED) {
+      if (seen_gemv) return fail(BTF_ERR_ARGS, "step: embedding ops come before every GEMV");
+      if (o.vec < 0 || o.vec >= nvec) return fail(BTF_ERR_ARGS, "step: vector index out of range");
+      if (vecs[o.vec].n % 1024) return fail(BTF_ERR_ARGS, "step: an embedded vector's length must be a multiple of 1024");
+      if (!o.table_codes || !o.table_scales || !o.d_tok) return fail(BTF_ERR_ARGS, "step: embedding needs its table and token");
+      if (misaligned(o.table_codes, 4) || misaligned(o.table_scales, 2))
+        return fail(BTF_ERR_ARGS, "step: embedding table codes must be 4-byte and scales 2-byte aligned");
+      if (o.hx.block < 0 || (o.hx.block > 0 && !pow2_upto(o.hx.block, 1024)))
+        return fail(BTF_ERR_ARGS, "step: hadamard block must be 0 or a power of two <= 1024");
+      if (writes[o.vec]) return fail(BTF_ERR_ARGS, "step: a vector is embedded at most once");
+      writes[o.vec]++;
+    } else if (o.kind == BTF_STEP_GEMV) {
+      seen_gemv = true;
+      if (const int rc = check_gemv_op(vecs, nvec, o)) return rc;
+      const btf_step_gemv& g = o.gemv;
       if (writes[g.in_vec] == 0 && !vecs[g.in_vec].data)
         return fail(BTF_ERR_ARGS, "step: a vector read before any write needs data");
       if (g.mode == BTF_GEMV_ADD && writes[g.out_vec] == 0 && !vecs[g.out_vec].data)
         return fail(BTF_ERR_ARGS, "step: a vector read before any write needs data");
-      if (vecs[g.in_vec].n % 32) return fail(BTF_ERR_ARGS, "step: quantized vectors need n % 32 == 0");
       writes[g.out_vec]++;
+    } else if (o.kind == BTF_STEP_ARGMAX) {
+      if (++picks > 1) return fail(BTF_ERR_ARGS, "step: at most one greedy pick per program");
+      if (o.vec < 0 || o.vec >= nvec) return fail(BTF_ERR_ARGS, "step: vector index out of range");
+      if (!o.d_tok_out) return fail(BTF_ERR_ARGS, "step: null token output");
+      if (i == 0 || ops[i - 1].kind != BTF_STEP_GEMV || ops[i - 1].gemv.out_vec != o.vec)
+        return fail(BTF_ERR_ARGS, "step: a greedy pick must directly follow the GEMV that writes its vector");
+    } else {
+      return fail(BTF_ERR_ARGS, "step: unknown op kind");
     }
   }
+  if (!seen_gemv) return fail(BTF_ERR_ARGS, "step: a program needs at least one GEMV");
   return BTF_OK;
 }
 
-int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, int ngemv, StepProgram** out,
-                const DevState& ds) {
-  if (const int rc = step_validate(vecs, nvec, gemvs, ngemv)) return rc;
+std::vector<btf_step_op> step_ops_of(const btf_step_gemv* gemvs, int ngemv) {
+  std::vector<btf_step_op> ops((size_t)ngemv);
+  for (int i = 0; i < ngemv; ++i) {
+    ops[i] = btf_step_op{};
+    ops[i].kind = BTF_STEP_GEMV;
+    ops[i].gemv = gemvs[i];
+  }
+  return ops;
+}
+
+int step_validate(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, int ngemv) {
+  const std::vector<btf_step_op> ops = step_ops_of(gemvs, ngemv);
+  return step_validate_ops(vecs, nvec, ops.data(), ngemv);
+}
+
+int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops, int nuops, StepProgram** out,
+                    const DevState& ds) {
+  if (const int rc = step_validate_ops(vecs, nvec, uops, nuops)) return rc;
   if (const int rc = step_check_residency(ds)) return rc;
   const int G = ds.cu_count;
-  // ---- which vectors need an initial quantize / an fp32 or Q8 copy
-  std::vector<bool> needs_init(nvec, false), needs_f32(nvec, false), needs_q8(nvec, false);
-  std::vector<int> final_writer(nvec, -1);  // GEMV index of each vector's last writer
-  {
-    std::vector<int> writes(nvec, 0);
-    for (int i = 0; i < ngemv; ++i) {
-      const btf_step_gemv& g = gemvs[i];
-      if (writes[g.in_vec] == 0) needs_init[g.in_vec] = true;
-      needs_q8[g.in_vec] = true;
-      if (g.mode == BTF_GEMV_ADD) {
-        if (writes[g.out_vec] == 0) needs_init[g.out_vec] = true;
-        needs_f32[g.out_vec] = true;
-      }
-      writes[g.out_vec]++;
-      final_writer[g.out_vec] = i;
+  if (G > 256) return fail(BTF_ERR_DEVICE, "step: more than 256 CUs");
+  // ---- versions of every vector over the program. Version 0 of a vector
+  // read before any write is its user data, published by a prologue op;
+  // every GEMV and embedding writes a new version of its output vector. A
+  // version has Q8 LL words if a GEMV without a prep reads it, fp32 LL words
+  // (with room for the block sums of squares) if an op wrote it (read later
+  // or not) or an add-mode GEMV or a GEMV with a prep reads it, and the sums
+  // of squares if a GEMV with a norm reads it.
+  struct Version {
+    int writer;                  // user op index, -1 = prologue
+    int last_q8_reader = -1;     // user op index
+    int last_f32_reader = -1;    // GEMV with a prep reading the fp32 words
+    std::vector<int> old_readers;  // add-mode GEMVs reading it as their old value
+    bool needs_sq = false;
+    int q8_slot = -1, f32_slot = -1;
+  };
+  std::vector<std::vector<Version>> versions(nvec);
+  std::vector<int> in_ver(nuops, -1), old_ver(nuops, -1), out_ver(nuops, -1);
+  int pick_gemv = -1;  // user index of the GEMV whose output the greedy pick reads
+  const btf_step_op* pick = nullptr;
+  for (int i = 0; i < nuops; ++i) {
+    const btf_step_op& o = uops[i];
+    if (o.kind == BTF_STEP_ARGMAX) {
+      pick = &o;
+      pick_gemv = i - 1;
+      continue;
     }
+    if (o.kind == BTF_STEP_EMBED) {
+      out_ver[i] = (int)versions[o.vec].size();
+      versions[o.vec].push_back(Version{i});
+      continue;
+    }
+    const btf_step_gemv& g = o.gemv;
+    if (versions[g.in_vec].empty()) versions[g.in_vec].push_back(Version{-1});
+    in_ver[i] = (int)versions[g.in_vec].size() - 1;
+    Version& iv = versions[g.in_vec].back();
+    if (has_prep(o)) {
+      iv.last_f32_reader = i;
+      iv.needs_sq |= o.normw != nullptr;
+    } else {
+      iv.last_q8_reader = i;
+    }
+    if (g.mode == BTF_GEMV_ADD) {
+      if (versions[g.out_vec].empty()) versions[g.out_vec].push_back(Version{-1});
+      old_ver[i] = (int)versions[g.out_vec].size() - 1;
+      versions[g.out_vec].back().old_readers.push_back(i);
+    }
+    out_ver[i] = (int)versions[g.out_vec].size();
+    versions[g.out_vec].push_back(Version{i});
   }
+  std::vector<int> final_writer(nvec, -1);
+  for (int v = 0; v < nvec; ++v)
+    if (!versions[v].empty()) final_writer[v] = versions[v].back().writer;
   StepProgram* P = new StepProgram();
   P->G = G;
   auto alloc = [&](size_t bytes) -> void* {
@@ -1035,32 +1476,6 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     step_destroy(P);
     return fail(code, msg);
   };
-  // ---- versions of every vector over the program (pre-pass). Version 0 of a
-  // vector read before any write is its user data, quantized by a prologue
-  // op; every GEMV writes a new version of its output vector. A version gets
-  // Q8 LL words only if a later op reads it as input; every GEMV output gets
-  // fp32 LL words (read by a later add-mode op as its old value, or not).
-  struct Version {
-    int writer;                 // GEMV index, -1 = prologue
-    int last_q8_reader = -1;    // GEMV index
-    std::vector<int> f32_readers;
-    int q8_slot = -1, f32_slot = -1;
-  };
-  std::vector<std::vector<Version>> versions(nvec);
-  std::vector<int> op_in_ver(ngemv), op_old_ver(ngemv, -1), op_out_ver(ngemv);
-  for (int v = 0; v < nvec; ++v)
-    if (needs_init[v]) versions[v].push_back(Version{-1});
-  for (int i = 0; i < ngemv; ++i) {
-    const btf_step_gemv& g = gemvs[i];
-    op_in_ver[i] = (int)versions[g.in_vec].size() - 1;
-    versions[g.in_vec].back().last_q8_reader = i;
-    if (g.mode == BTF_GEMV_ADD) {
-      op_old_ver[i] = (int)versions[g.out_vec].size() - 1;
-      versions[g.out_vec].back().f32_readers.push_back(i);
-    }
-    op_out_ver[i] = (int)versions[g.out_vec].size();
-    versions[g.out_vec].push_back(Version{i});
-  }
   // kSlots buffers of each kind per vector, taken in turn by the versions
   // that need one, so a version overwrites the one kSlots such versions
   // earlier (whose readers have long finished, normally).
@@ -1073,20 +1488,35 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     int nq = 0, nf = 0;
     for (Version& ve : versions[v]) {
       if (ve.last_q8_reader >= 0) ve.q8_slot = nq++ % kSlots;
-      // every GEMV's result is written to device memory (fp32 words), read
-      // later or not; the prologue's version 0 only if an add reads it
-      if (ve.writer >= 0 || !ve.f32_readers.empty()) ve.f32_slot = nf++ % kSlots;
+      if (ve.writer >= 0 || !ve.old_readers.empty() || ve.last_f32_reader >= 0) ve.f32_slot = nf++ % kSlots;
     }
+    const size_t n = (size_t)vecs[v].n, nb = (n + 31) / 32;
     for (int b = 0; b < kSlots && b < nq; ++b)
-      if (!(q8buf[b][v] = static_cast<uint64_t*>(alloc((size_t)(vecs[v].n / 32) * kWordsPerBlock * 8))))
+      if (!(q8buf[b][v] = static_cast<uint64_t*>(alloc(nb * kWordsPerBlock * 8))))
         return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
     for (int b = 0; b < kSlots && b < nf; ++b)
-      if (!(f32buf[b][v] = static_cast<uint64_t*>(alloc((size_t)vecs[v].n * 8))))
+      if (!(f32buf[b][v] = static_cast<uint64_t*>(alloc((n + 2 * nb) * 8))))
         return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
   }
   auto q8_of = [&](int v, int k) { return versions[v][k].q8_slot >= 0 ? q8buf[versions[v][k].q8_slot][v] : nullptr; };
   auto f32_of = [&](int v, int k) { return versions[v][k].f32_slot >= 0 ? f32buf[versions[v][k].f32_slot][v] : nullptr; };
-  // ---- the device program: prologue quantize ops, then the GEMVs in order
+  std::vector<PrepDev> preps;
+  auto add_prep = [&](const float* normw, float eps, const btf_hx& hx) {
+    PrepDev p{};
+    p.normw = normw;
+    p.eps = eps;
+    p.block = hx.block > 0 ? hx.block : 0;
+    p.hs = hx.block > 0 ? 1.0f / std::sqrt((float)hx.block) : 1.0f;
+    p.signs = hx.block > 0 ? hx.signs : nullptr;
+    if (hx.block > 0 && hx.perm_rep > 1) {
+      p.hd = hx.perm_hd;
+      p.nk = hx.perm_nk;
+      p.rep = hx.perm_rep;
+    }
+    preps.push_back(p);
+    return (int)preps.size() - 1;
+  };
+  // ---- the device program: prologue quantize ops, embeddings, then the GEMVs in order
   std::vector<OpDev> ops;
   // known[v * G + w]: the last GEMV whose barrier B workgroup w has surely
   // passed, as far as workgroup v can tell when it reaches a later op. A
@@ -1098,7 +1528,7 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
   int last_gemv = -1;                   // device index of the previous GEMV
   std::vector<int> prev_gemv;           // per device op: the GEMV before it (-1: none)
   auto owns = [&](const OpDev& x, int w) { return (w - x.rot + G) % G < x.units; };
-  std::vector<int> dev_of(ngemv, -1);        // device op index of each GEMV
+  std::vector<int> dev_of(nuops, -1);        // device op index of each user op
   std::vector<int> prologue_of(nvec, -1);    // device op index of each prologue op
   // Unit placement: unit u of an op goes to workgroup (u + rot) % G. An
   // add-mode op takes the rotation of the op that wrote its old value when
@@ -1108,7 +1538,6 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
   // lowest.
   std::vector<double> load(G, 0.0);
   auto place = [&](OpDev& o, double cost_per_unit, int align_to) {
-    o.units = (o.N + 31) / 32;
     const int extra = o.units % G;
     int best = 0;
     if (align_to >= 0 && ops[align_to].units == o.units) {
@@ -1134,17 +1563,44 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     }
   };
   for (int v = 0; v < nvec; ++v) {
-    if (!needs_init[v]) continue;
+    if (versions[v].empty() || versions[v][0].writer >= 0) continue;
     OpDev o{};
     o.kind = 0;
     o.N = vecs[v].n;
+    o.units = (o.N + 31) / 32;
     o.src = vecs[v].data;
     o.out_q8 = q8_of(v, 0);
     o.out_f32 = f32_of(v, 0);
+    o.out_sq = versions[v][0].needs_sq;
+    o.my_tag = (uint32_t)ops.size() + 1;
+    o.war_op = -1;
+    o.prep = -1;
+    place(o, 1.0, -1);
+    prologue_of[v] = (int)ops.size();
+    ops.push_back(o);
+    prev_gemv.push_back(-1);
+  }
+  for (int i = 0; i < nuops; ++i) {
+    const btf_step_op& u = uops[i];
+    if (u.kind != BTF_STEP_EMBED) continue;
+    const int v = u.vec;
+    const Version& ve = versions[v][out_ver[i]];
+    OpDev o{};
+    o.kind = 2;
+    o.N = vecs[v].n;
+    o.units = o.N / kSliceVals;
+    o.codes = u.table_codes;
+    o.scales = u.table_scales;
+    o.src = u.d_tok;
+    o.prep = add_prep(nullptr, 0.0f, u.hx);
+    o.out_plain = final_writer[v] == i ? vecs[v].data : nullptr;
+    o.out_q8 = q8_of(v, out_ver[i]);
+    o.out_f32 = f32_of(v, out_ver[i]);
+    o.out_sq = ve.needs_sq;
     o.my_tag = (uint32_t)ops.size() + 1;
     o.war_op = -1;
     place(o, 1.0, -1);
-    prologue_of[v] = (int)ops.size();
+    dev_of[i] = (int)ops.size();
     ops.push_back(o);
     prev_gemv.push_back(-1);
   }
@@ -1152,8 +1608,10 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     const int w = versions[v][k].writer;
     return w < 0 ? prologue_of[v] : dev_of[w];
   };
-  for (int i = 0; i < ngemv; ++i) {
-    const btf_step_gemv& g = gemvs[i];
+  for (int i = 0; i < nuops; ++i) {
+    const btf_step_op& u = uops[i];
+    if (u.kind != BTF_STEP_GEMV) continue;
+    const btf_step_gemv& g = u.gemv;
     const int me = (int)ops.size();
     dev_of[i] = me;
     OpDev o{};
@@ -1161,21 +1619,25 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     o.mode = g.mode;
     o.K = g.K;
     o.N = g.N;
+    o.units = (g.N + 31) / 32;
     o.cpr = g.K / 64;
     o.qpu_log2 = g.mode == BTF_GEMV_SWIGLU ? 4 : 3;
     o.codes = g.codes;
     o.scales = g.scales;
     o.up_codes = g.up_codes;
     o.up_scales = g.up_scales;
-    o.in_q8 = q8_of(g.in_vec, op_in_ver[i]);
-    o.in_tag = (uint32_t)dev_writer(g.in_vec, op_in_ver[i]) + 1;
+    const bool pre = has_prep(u);
+    o.prep = pre ? add_prep(u.normw, u.eps, u.hx) : -1;
+    o.in_ll = pre ? f32_of(g.in_vec, in_ver[i]) : q8_of(g.in_vec, in_ver[i]);
+    o.in_tag = (uint32_t)dev_writer(g.in_vec, in_ver[i]) + 1;
+    o.argmax = i == pick_gemv;
     int align_to = -1;
     if (g.mode == BTF_GEMV_ADD) {
-      o.old_f32 = f32_of(g.out_vec, op_old_ver[i]);
-      o.old_tag = (uint32_t)dev_writer(g.out_vec, op_old_ver[i]) + 1;
-      align_to = dev_writer(g.out_vec, op_old_ver[i]);
+      o.old_f32 = f32_of(g.out_vec, old_ver[i]);
+      o.old_tag = (uint32_t)dev_writer(g.out_vec, old_ver[i]) + 1;
+      align_to = dev_writer(g.out_vec, old_ver[i]);
     }
-    const int kv = op_out_ver[i];
+    const int kv = out_ver[i];
     const Version& nv = versions[g.out_vec][kv];
     // Plain output: only the final version goes to the user's buffer (plain
     // stores of two ops to one address from different XCDs reach HBM in the
@@ -1183,6 +1645,7 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     o.out_plain = final_writer[g.out_vec] == i ? vecs[g.out_vec].data : nullptr;
     o.out_q8 = q8_of(g.out_vec, kv);
     o.out_f32 = f32_of(g.out_vec, kv);
+    o.out_sq = nv.needs_sq;
     o.my_tag = (uint32_t)me + 1;
     place(o, (double)g.K * (g.mode == BTF_GEMV_SWIGLU ? 2 : 1), align_to);
     // Write-after-read: the buffers this version takes held the version
@@ -1192,27 +1655,29 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     // program order. The final writer also stores into the user's buffer,
     // which the prologue read (version 0): after every reader of version 0.
     int war = -1;
+    auto dev_reader = [&](int r) { return r >= 0 ? dev_of[r] : -1; };
     for (int k = kv - 1; k >= 0; --k) {
       const Version& pv = versions[g.out_vec][k];
       if (nv.q8_slot >= 0 && pv.q8_slot == nv.q8_slot) {
-        war = std::max(war, pv.last_q8_reader >= 0 ? dev_of[pv.last_q8_reader] : -1);
+        war = std::max(war, dev_reader(pv.last_q8_reader));
         break;
       }
     }
     for (int k = kv - 1; k >= 0; --k) {
       const Version& pv = versions[g.out_vec][k];
       if (nv.f32_slot >= 0 && pv.f32_slot == nv.f32_slot) {
-        for (int r : pv.f32_readers) {
+        war = std::max(war, dev_reader(pv.last_f32_reader));
+        for (int r : pv.old_readers) {
           const OpDev& ro = ops[dev_of[r]];
           if (!(ro.units == o.units && ro.rot == o.rot)) war = std::max(war, dev_of[r]);
         }
         break;
       }
     }
-    if (o.out_plain && needs_init[g.out_vec]) {
+    if (o.out_plain && versions[g.out_vec][0].writer < 0) {
       const Version& v0 = versions[g.out_vec][0];
-      int last = v0.last_q8_reader;
-      for (int r : v0.f32_readers) last = std::max(last, r);
+      int last = std::max(v0.last_q8_reader, v0.last_f32_reader);
+      for (int r : v0.old_readers) last = std::max(last, r);
       if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
     }
     if (war >= 0) {  // implied for every workgroup that writes this op's output?
@@ -1249,11 +1714,12 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     prev_gemv.push_back(last_gemv);
     last_gemv = me;
   }
-  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 384 ops (quantize prologue + GEMVs)");
+  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 384 ops (prologue + GEMVs)");
   // Early fetch and carry. An op's input is fetched by the I/O waves while
   // the previous GEMV computes when every producer it reads from comes
   // before that previous GEMV (a workgroup then never waits for its own
-  // unpublished output). An add-mode op whose old value was produced by the
+  // unpublished output) and it is a plain Q8 input (a prep runs in the
+  // compute waves). An add-mode op whose old value was produced by the
   // previous GEMV with the same unit placement takes it from the LDS carry
   // (the same workgroup computed it) -- unless that GEMV is a swiglu, whose
   // epilogue keeps its rows in another layout and writes no carry.
@@ -1270,7 +1736,7 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
       const bool in_ok = (int)o.in_tag - 1 < pd;
       const bool no_old = o.mode != BTF_GEMV_ADD || o.carry_in;
       const bool fits = (o.K / 32) * kWordsPerBlock <= kIL * kEIn;  // one round of the I/O waves
-      o.early = pd >= 0 && in_ok && no_old && fits;
+      o.early = pd >= 0 && in_ok && no_old && fits && o.prep < 0;
       pd = d;
     }
   }
@@ -1283,18 +1749,38 @@ int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, 
     }
     P->first = nxt;
   }
+  HeadDev head{};
+  if (pick) {
+    head.present = 1;
+    head.tag = (uint32_t)dev_of[pick_gemv] + 1;
+    head.tok_out = pick->d_tok_out;
+    head.pos = pick->d_pos;
+    if (!(head.parts = static_cast<uint64_t*>(alloc((size_t)G * 2 * 8))))
+      return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
+  }
+  if (preps.empty()) preps.push_back(PrepDev{});
   P->nops = (int)ops.size();
   if (!(P->d_ops = static_cast<OpDev*>(alloc(ops.size() * sizeof(OpDev)))) ||
       !(P->d_ctl = static_cast<Ctl*>(alloc(sizeof(Ctl)))) ||
-      !(P->d_cnt = static_cast<uint32_t*>(alloc(ops.size() * sizeof(uint32_t)))))
+      !(P->d_cnt = static_cast<uint32_t*>(alloc(ops.size() * sizeof(uint32_t)))) ||
+      !(P->d_preps = static_cast<PrepDev*>(alloc(preps.size() * sizeof(PrepDev)))) ||
+      !(P->d_head = static_cast<HeadDev*>(alloc(sizeof(HeadDev)))))
     return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
   const Ctl c0{1u, 0u, 0u, 0u};
   if (hipMemcpy(P->d_ops, ops.data(), ops.size() * sizeof(OpDev), hipMemcpyHostToDevice) != hipSuccess ||
-      hipMemcpy(P->d_ctl, &c0, sizeof c0, hipMemcpyHostToDevice) != hipSuccess)
+      hipMemcpy(P->d_ctl, &c0, sizeof c0, hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(P->d_preps, preps.data(), preps.size() * sizeof(PrepDev), hipMemcpyHostToDevice) != hipSuccess ||
+      hipMemcpy(P->d_head, &head, sizeof head, hipMemcpyHostToDevice) != hipSuccess)
     return bail(BTF_ERR_LAUNCH, "step: program upload failed");
   (void)hipGetDevice(&P->device);
   *out = P;
   return BTF_OK;
+}
+
+int step_create(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs, int ngemv, StepProgram** out,
+                const DevState& ds) {
+  const std::vector<btf_step_op> ops = step_ops_of(gemvs, ngemv);
+  return step_create_ops(vecs, nvec, ops.data(), ngemv, out, ds);
 }
 
 int step_set_spin_limit(StepProgram* P, uint32_t polls) {
@@ -1321,7 +1807,7 @@ int step_launch(StepProgram* P, hipStream_t st) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev != P->device)
     return fail(BTF_ERR_ARGS, "step: launch on a device other than the program's");
-  void* args[] = {&P->d_ops, &P->nops, &P->first, &P->d_ctl, &P->d_cnt};
+  void* args[] = {&P->d_ops, &P->nops, &P->first, &P->d_ctl, &P->d_cnt, &P->d_preps, &P->d_head};
   const hipError_t e =
       hipLaunchCooperativeKernel(reinterpret_cast<const void*>(step_kernel), dim3(P->G), dim3(kThreads), args, 0, st);
   if (e != hipSuccess) return fail(BTF_ERR_LAUNCH, std::string("step kernel: ") + hipGetErrorString(e));

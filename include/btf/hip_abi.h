@@ -215,6 +215,46 @@ int btf_hip_step_destroy(btf_step_t prog);
  * makes a launch give up waiting and set the error flag instead of hanging. */
 int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls);
 
+/* A whole batch-1 decode step in one launch: the step program with the ops
+ * either side of the GEMV chain and each GEMV's full input prep. It replaces
+ * the reference decoder's per-token graph (src/cuda/gpu_decoder.cu:401-421,
+ * 452-486: launch_embed, then per GEMV launch_prep + launch_gemv, then
+ * launch_argmax and launch_pos_add) for the parts of the step on this path.
+ *  - BTF_STEP_GEMV: `gemv` as in btf_hip_step_create, its input first put
+ *    through launch_prep's pipeline (src/cuda/kernels.cuh:40-43): RMSNorm *
+ *    normw (NULL: none, eps its epsilon), then the transform hx (block 0:
+ *    none; a power of two <= 1024; perm_hd * perm_nk * perm_rep == K when
+ *    perm_rep > 1; signs NULL or [K]), then Q8_0. With a norm or transform
+ *    the input vector's length must equal K. Bit-identical to launch_prep +
+ *    launch_gemv.
+ *  - BTF_STEP_EMBED: vector `vec` (length E, a multiple of 1024) = row
+ *    *d_tok of the packed table (table_codes [V][E/4], table_scales
+ *    [V][E/128], device or mapped host memory) with the inverse transform hx
+ *    (launch_embed, src/cuda/kernels.cuh:82-85). Embed ops come before every
+ *    GEMV. d_tok is read when the launch starts.
+ *  - BTF_STEP_ARGMAX: *d_tok_out = the greedy pick over vector `vec`
+ *    (launch_argmax: the smallest index on ties, a NaN never wins), then, if
+ *    d_pos is set, *d_pos += 1 (launch_pos_add). It must directly follow the
+ *    GEMV that writes `vec`; at most one per program. d_tok_out may be the
+ *    embed op's d_tok: each launch then decodes the token the previous one
+ *    picked.
+ * Unused fields are ignored. */
+enum { BTF_STEP_GEMV = 0, BTF_STEP_EMBED = 1, BTF_STEP_ARGMAX = 2 };
+typedef struct btf_step_op {
+  int kind;
+  btf_step_gemv gemv;           /* GEMV */
+  const float* normw;           /* GEMV: RMSNorm weight [K] or NULL */
+  float eps;                    /* GEMV: RMSNorm epsilon */
+  btf_hx hx;                    /* GEMV: input transform; EMBED: inverse transform */
+  int vec;                      /* EMBED: output vector; ARGMAX: logits vector */
+  const uint8_t* table_codes;   /* EMBED */
+  const uint16_t* table_scales; /* EMBED */
+  const int* d_tok;             /* EMBED: token id (device) */
+  int* d_tok_out;               /* ARGMAX: picked token (device) */
+  int* d_pos;                   /* ARGMAX: position counter (device) or NULL */
+} btf_step_op;
+int btf_hip_step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, btf_step_t* out);
+
 /* ---- load path: GGUF reader -> pinned double-buffered staging -> repack --
  * The reference decoder reads its model with bd::Gguf
  * (ref/bonsai-decoder/include/bd/gguf.hpp:49-85, src/gguf.cpp:73-147),

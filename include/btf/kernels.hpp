@@ -134,6 +134,10 @@ class StepProgram {
   StepProgram(const btf_step_vec* vecs, int nvec, const btf_step_gemv* ops, int nops) {
     detail::check(btf_hip_step_create(vecs, nvec, ops, nops, &p_), "step_create");
   }
+  // a whole token: embed ops, GEMVs with their full input prep, the greedy pick
+  StepProgram(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops) {
+    detail::check(btf_hip_step_create_ops(vecs, nvec, ops, nops, &p_), "step_create_ops");
+  }
   StepProgram(const StepProgram&) = delete;
   StepProgram& operator=(const StepProgram&) = delete;
   ~StepProgram() { (void)btf_hip_step_destroy(p_); }

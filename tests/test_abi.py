@@ -140,6 +140,48 @@ def test_invalid_arguments_rejected_on_host():
     assert h.step_create_raw([], []) == ARGS
 
 
+def test_whole_token_programs_checked_on_host():
+    """btf_hip_step_create_ops rejects malformed whole-token programs before
+    any HIP call (BTF_ERR_ARGS); a valid one only fails for want of a device."""
+    import btf_hip as h
+    ARGS = h.BTF_ERR_ARGS
+    G = h.GemvMode
+    codes, scales, y, tok = 0x100000, 0x200000, 0x300000, 0x400000
+    E, F, V = 2048, 3072, 4000
+    vecs = [h.StepVec(E, y), h.StepVec(F, None), h.StepVec(V, y + 0x10000)]
+    emb = h.StepEmbed(0, codes, scales, tok, h.Hx(block=1024))
+    up = h.StepGemv(G.kStore, E, F, codes, scales, 0, 1, normw=y, eps=1e-6, hx=h.Hx(block=256))
+    down = h.StepGemv(G.kAdd, F, E, codes, scales, 1, 0, hx=h.Hx(block=1024))
+    head = h.StepGemv(G.kStore, E, V, codes, scales, 0, 2, normw=y, eps=1e-6)
+    pick = h.StepArgmax(2, tok, tok + 4)
+    good = [emb, up, down, head, pick]
+    assert h.step_create_ops_raw(vecs, good) == h.BTF_ERR_NOT_INIT  # valid: needs a device
+    bad = {
+        "embed after a GEMV": [up, emb, down, head, pick],
+        "embed width": ([h.StepVec(1536, y)] + vecs[1:], [h.StepEmbed(0, codes, scales, tok), up]),
+        "embed table": [h.StepEmbed(0, None, scales, tok), up],
+        "embed token": [h.StepEmbed(0, codes, scales, None), up],
+        "embed table alignment": [h.StepEmbed(0, codes + 2, scales, tok), up],
+        "embed block": [h.StepEmbed(0, codes, scales, tok, h.Hx(block=96)), up],
+        "embedded twice": [emb, h.StepEmbed(0, codes, scales, tok), up],
+        "pick not after its GEMV": [emb, up, down, pick, head],
+        "pick of another vector": [emb, up, down, head, h.StepArgmax(1, tok)],
+        "two picks": [emb, up, down, head, pick, pick],
+        "pick output": [emb, up, down, head, h.StepArgmax(2, None)],
+        "prep input length": [emb, h.StepGemv(G.kStore, 1024, F, codes, scales, 0, 1, normw=y)],
+        "prep block": [emb, h.StepGemv(G.kStore, E, F, codes, scales, 0, 1, hx=h.Hx(block=2048))],
+        "prep block power of two": [emb, h.StepGemv(G.kStore, E, F, codes, scales, 0, 1, hx=h.Hx(block=384))],
+        "perm geometry": [emb, h.StepGemv(G.kStore, E, F, codes, scales, 0, 1, hx=h.Hx(1024, 32, 16, 2))],
+        "perm tile": [emb, h.StepGemv(G.kStore, E, F, codes, scales, 0, 1, hx=h.Hx(1024, 8, 128, 2))],
+        "unknown kind": [emb, up, 7],
+        "no GEMV": [emb],
+    }
+    for what, prog in bad.items():
+        v, ops = prog if isinstance(prog, tuple) else (vecs, prog)
+        assert h.step_create_ops_raw(v, ops) == ARGS, what
+        assert h.last_error(), what
+
+
 def _compile_and_run(tmp_path, name, src, compiler, std):
     cc = shutil.which(compiler)
     if cc is None:
