@@ -105,6 +105,7 @@ _launch_gemv = _decl("btf_hip_launch_gemv", [C.POINTER(_GemvSeg), _i, _i, _i, C.
 _launch_embed = _decl("btf_hip_launch_embed", [_vp, _vp, _vp, _i, _i, C.POINTER(_Hx), _vp, _vp])
 _argmax_part_bytes = _decl("btf_hip_argmax_part_bytes", [_i], _i64)
 _launch_argmax = _decl("btf_hip_launch_argmax", [_vp, _i, _vp, _vp, _vp])
+_launch_argmax_noalloc = _decl("btf_hip_launch_argmax_noalloc", [_vp, _i, _vp, _vp])
 _launch_pos_add = _decl("btf_hip_launch_pos_add", [_vp, _i, _vp])
 _launch_gemv_ex = _decl("btf_hip_launch_gemv_ex", [C.POINTER(_GemvSeg), _i, _i, _i, C.POINTER(_Q8Act), _vp, _i, _i,
                                                     C.POINTER(_Q8Act), _vp])
@@ -153,7 +154,7 @@ _loader_destroy = _decl("btf_hip_loader_destroy", [_vp])
 ABI_SYMBOLS = (
     "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
     "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_launch_gemv_ptq1_0", "btf_hip_launch_embed", "btf_hip_argmax_part_bytes",
-    "btf_hip_launch_argmax", "btf_hip_launch_pos_add", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
+    "btf_hip_launch_argmax", "btf_hip_launch_argmax_noalloc", "btf_hip_launch_pos_add", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
     "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
     "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
     "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
@@ -298,6 +299,16 @@ def launch_argmax(logits, V: int, part, d_tok_out, stream=None) -> None:
 
 def launch_argmax_raw(logits, V, part, d_tok_out, stream=None) -> int:
     return _launch_argmax(_addr(logits), V, _addr(part), _addr(d_tok_out), _stream(stream))
+
+
+def launch_argmax_noalloc(logits, V: int, d_tok_out, stream=None) -> None:
+    """launch_argmax without a workspace: the library's static per-GPU scratch
+    (concurrent calls on one GPU race)."""
+    _check(_launch_argmax_noalloc(_addr(logits), V, _addr(d_tok_out), _stream(stream)))
+
+
+def launch_argmax_noalloc_raw(logits, V, d_tok_out, stream=None) -> int:
+    return _launch_argmax_noalloc(_addr(logits), V, _addr(d_tok_out), _stream(stream))
 
 
 def launch_pos_add(d_pos, M: int, stream=None) -> None:

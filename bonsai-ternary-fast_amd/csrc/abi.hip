@@ -136,6 +136,14 @@ int btf_hip_kernels_init(int device) {
   s->cu_count = p.multiProcessorCount;
   s->lds_per_block = (int)p.sharedMemPerBlock;
   s->max_threads = p.maxThreadsPerBlock;
+  if (!s->argmax_scratch) {  // the static scratch's address on this device (with the device current)
+    int cur = -1;
+    if (hipGetDevice(&cur) != hipSuccess) return fail(BTF_ERR_DEVICE, "kernels_init: hipGetDevice");
+    if (cur != device && hipSetDevice(device) != hipSuccess) return fail(BTF_ERR_DEVICE, "kernels_init: hipSetDevice");
+    const int rc = argmax_scratch_setup(*s);
+    if (cur != device) (void)hipSetDevice(cur);
+    if (rc != BTF_OK) return rc;
+  }
   s->init = true;
   return BTF_OK;
 }
@@ -207,6 +215,14 @@ int btf_hip_launch_argmax(const float* logits, int V, void* part, int* d_tok_out
   const DevState* ds = current_state();
   if (!ds) return BTF_ERR_NOT_INIT;
   return argmax(logits, V, part, d_tok_out, static_cast<hipStream_t>(stream));
+}
+
+int btf_hip_launch_argmax_noalloc(const float* logits, int V, int* d_tok_out, btf_stream_t stream) {
+  if (!logits || !d_tok_out) return fail(BTF_ERR_ARGS, "argmax_noalloc: null pointer");
+  if (V <= 0) return fail(BTF_ERR_ARGS, "argmax_noalloc: empty vocabulary");
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  return argmax_noalloc(logits, V, d_tok_out, static_cast<hipStream_t>(stream), *ds);
 }
 
 int btf_hip_launch_pos_add(int* d_pos, int M, btf_stream_t stream) {

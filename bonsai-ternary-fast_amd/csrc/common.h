@@ -22,6 +22,7 @@ struct DevState {
   int cu_count = 0;
   int lds_per_block = 0;
   int max_threads = 0;
+  void* argmax_scratch = nullptr;  // this device's copy of the no-allocation pick's static scratch
 };
 DevState* dev_state(int device);  // nullptr if device id out of range
 // State of the current device, or nullptr (with the error set) if
@@ -190,6 +191,8 @@ int embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M,
           float* x, hipStream_t st);
 int64_t argmax_part_bytes(int V);
 int argmax(const float* logits, int V, void* part, int* out, hipStream_t st);
+int argmax_scratch_setup(DevState& ds);  // with the device current
+int argmax_noalloc(const float* logits, int V, int* out, hipStream_t st, const DevState& ds);
 int pos_add(int* d_pos, int M, hipStream_t st);
 
 }  // namespace btfhip

@@ -26,6 +26,7 @@
 //    one wave over the parts. A NaN never wins; all-NaN gives 0.
 //  * pos_add: *d_pos += M, as a vector atomic (src/cuda/kernels.cuh:92).
 #include <cmath>
+#include <string>
 
 #include "../../include/btf/hip_abi.h"
 #include "common.h"
@@ -145,6 +146,29 @@ int argmax_parts_of(int V, int* per) {
   return n;
 }
 }  // namespace
+
+// The no-allocation greedy pick's scratch: one key per part, at most
+// kArgMaxParts parts whatever V. Each GPU holds its own copy until the
+// process ends; host code uses the address hipGetSymbolAddress gave for the
+// device (set up by kernels_init), never this name.
+static __device__ __align__(256) uint64_t scratch[kArgMaxParts];
+
+int argmax_scratch_setup(DevState& ds) {
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    return fail(BTF_ERR_DEVICE, std::string("argmax scratch: hipGetSymbolAddress: ") + hipGetErrorString(e));
+  ds.argmax_scratch = p;
+  return BTF_OK;
+}
+
+int argmax_noalloc(const float* logits, int V, int* out, hipStream_t st, const DevState& ds) {
+  int per;
+  const int n = argmax_parts_of(V, &per);
+  if (n > kArgMaxParts) return fail(BTF_ERR_ARGS, "argmax_noalloc: more parts than the static scratch holds");
+  if (!ds.argmax_scratch) return fail(BTF_ERR_NOT_INIT, "argmax_noalloc: scratch not set up for this device");
+  return argmax(logits, V, ds.argmax_scratch, out, st);
+}
 
 int64_t argmax_part_bytes(int V) {
   int per;

@@ -93,6 +93,12 @@ inline size_t argmax_part_bytes(int V) { return (size_t)btf_hip_argmax_part_byte
 inline void launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t st) {
   detail::check(btf_hip_launch_argmax(logits, V, part, d_tok_out, st), "launch_argmax");
 }
+// no counterpart in kernels.cuh: launch_argmax without a workspace, for
+// callers that cannot allocate (the library's static per-GPU scratch;
+// overlapping calls on one GPU race)
+inline void launch_argmax_noalloc(const float* logits, int V, int* d_tok_out, btf_stream_t st) {
+  detail::check(btf_hip_launch_argmax_noalloc(logits, V, d_tok_out, st), "launch_argmax_noalloc");
+}
 
 // kernels.cuh:92
 inline void launch_pos_add(int* d_pos, int M, btf_stream_t st) {
