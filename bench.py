@@ -87,15 +87,18 @@ def prep_bytes(K, M):
 class Setup:
     """Weights of every matrix of the sweep, resident in one device arena."""
 
-    def __init__(self, hip, torch, layers, seed=0, keep_src=False):
+    def __init__(self, hip, torch, layers, seed=0, keep_src=False, with_embed=False):
         """keep_src: also keep every matrix's PTQ1_0 rows resident (for the
-        GEMV that reads them directly)."""
+        GEMV that reads them directly). with_embed: also a packed embedding
+        table of the output projection's shape (V x 5120, matrix id 321)."""
         self.hip, self.torch = hip, torch
         shapes = []  # (name, layer, N, K, matrix id)
         for l in range(layers):
             shapes += [("qkv", l, QKV, E, 5 * l), ("o", l, E, E, 5 * l + 1), ("gate", l, F, E, 5 * l + 2),
                        ("up", l, F, E, 5 * l + 3), ("down", l, E, F, 5 * l + 4)]
         shapes.append(("output", layers, V, E, 5 * 64))
+        if with_embed:
+            shapes.append(("embed", layers, V, E, 5 * 64 + 1))
         off, self.mats = 0, {}
         for name, l, N, K, mid in shapes:
             co = off
@@ -108,21 +111,24 @@ class Setup:
         base = self.arena.data_ptr()
         self.src_off, soff = {}, 0
         for key, (N, K, _, _, _) in self.mats.items():
+            if key[0] == "embed":
+                continue
             self.src_off[key] = soff
             soff = align(soff + N * K // 128 * 28)
         self.src = torch.empty(soff if keep_src else 0, dtype=torch.uint8, device="cuda")
         maxblk = max(N * K // 128 for N, K, _, _, _ in self.mats.values())
-        stage = torch.empty(0 if keep_src else maxblk * 28, dtype=torch.uint8, device="cuda")
+        stage = torch.empty(maxblk * 28 if (not keep_src or with_embed) else 0, dtype=torch.uint8, device="cuda")
         st = torch.cuda.current_stream().cuda_stream
         t0 = time.time()
         for (name, l), (N, K, mid, co, so) in self.mats.items():
             nb = N * K // 128
-            src = self.src.data_ptr() + self.src_off[(name, l)] if keep_src else stage.data_ptr()
+            src = self.src.data_ptr() + self.src_off[(name, l)] if keep_src and name != "embed" else stage.data_ptr()
             hip.gen_ptq1_0(seed, mid, 0, nb, src, st)
             hip.launch_repack(src, nb, base + co, base + so, st)
         torch.cuda.synchronize()
         self.setup_s = time.time() - t0
-        self.weight_bytes = sum(N * K // 4 + N * K // 64 for N, K, _, _, _ in self.mats.values())
+        self.weight_bytes = sum(N * K // 4 + N * K // 64 for (name, _), (N, K, _, _, _) in self.mats.items()
+                                if name != "embed")
         del stage
 
     def seg(self, name, l, y, ldy):
@@ -314,6 +320,222 @@ class Step:
             self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
         else:
             self.gemv([S.seg("output", self.layers, self.logits, V)], E, 1, G.kStore, st)
+
+
+class Token:
+    """One whole decode step of the 27B shapes at batch 1, as the reference
+    decoder runs it (src/cuda/gpu_decoder.cu:401-421, 452-486) minus the
+    attention itself: the embedding lookup of the current token (inverse
+    FWHT 1024 + signs), 64 x (QKV through the attention RMSNorm + FWHT 1024 +
+    signs; o += W_o * (attention-output stand-in through FWHT 1024 + signs);
+    gate/up swiglu through the FFN RMSNorm + FWHT 1024 + signs; down += through
+    FWHT 1024 + signs), the output projection through the output RMSNorm +
+    FWHT 1024 + signs, the greedy pick into the token and the position
+    counter. Each step decodes the token the previous one picked. Seeded norm
+    weights N(1, 0.1) and random signs; the weights are the sweep's."""
+
+    BLOCK = 1024
+
+    def __init__(self, S: Setup, layers, seed=1):
+        import numpy as np
+        hip, torch = S.hip, S.torch
+        self.S, self.layers = S, layers
+        rng = np.random.default_rng(seed)
+        dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+        sg = lambda n: dev(np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float32))
+        nw = lambda n: dev((1.0 + 0.1 * rng.standard_normal(n)).astype(np.float32))
+        self.norm = [(nw(E), nw(E)) for _ in range(layers)]              # attention, FFN
+        self.signs = [(sg(E), sg(E), sg(E), sg(F)) for _ in range(layers)]  # qkv, o, gate/up, down inputs
+        self.out_norm, self.out_signs, self.emb_signs = nw(E), sg(E), sg(E)
+        z = lambda n: torch.zeros(n, dtype=torch.float32, device="cuda")
+        self.res, self.qkv, self.h, self.logits = z(E), z(QKV), z(F), z(V)
+        self.att = dev((rng.standard_normal(E) * 2).astype(np.float32))
+        self.tok0 = 7
+        self.tok = dev(np.array([self.tok0], np.int32))
+        self.pos = torch.zeros(1, dtype=torch.int32, device="cuda")
+        self.act = hip.Q8Act(torch.zeros(F, dtype=torch.int8, device="cuda"),
+                             torch.zeros(F // 32, dtype=torch.float32, device="cuda"),
+                             torch.zeros(F // 32, dtype=torch.int32, device="cuda"))
+        self.part = torch.zeros(hip.argmax_part_bytes(V) // 4, dtype=torch.int32, device="cuda")
+        # algorithmic bytes: the embedding row and its output; per GEMV the
+        # weights, the prep (fp32 input, norm weights, signs, the Q8 written
+        # and read) and the outputs; the logits read by the pick
+        prep_b = lambda K, norm: 4 * K + 2 * (K + K // 4) + 4 * K + (4 * K if norm else 0)
+        per_layer = (gemv_bytes(QKV, E, 1) - (E + E // 4) + prep_b(E, True) +
+                     gemv_bytes(E, E, 1, 2) - (E + E // 4) + prep_b(E, False) +
+                     gemv_bytes(F, E, 1, 1, 2) - (E + E // 4) + prep_b(E, True) +
+                     gemv_bytes(E, F, 1, 2) - (F + F // 4) + prep_b(F, False))
+        self.total_bytes = (E // 4 + E // 64 + 4 * E + layers * per_layer +
+                            gemv_bytes(V, E, 1) - (E + E // 4) + prep_b(E, True) + 4 * V)
+
+    def reset(self):
+        self.tok.fill_(self.tok0)
+        self.pos.zero_()
+
+    def hx(self, signs):
+        return self.S.hip.Hx(block=self.BLOCK, signs=signs)
+
+    def ops(self):
+        """The step program's ops. Vector slots: 0 residual, 1 qkv, 2
+        attention-output stand-in, 3 h, 4 logits."""
+        hip, S, G = self.S.hip, self.S, self.S.hip.GemvMode
+        base = S.arena.data_ptr()
+
+        def w(name, l):
+            N, K, _, co, so = S.mats[(name, l)]
+            return base + co, base + so
+
+        ops = [hip.StepEmbed(0, *w("embed", self.layers), self.tok, self.hx(self.emb_signs))]
+        for l in range(self.layers):
+            na, nf = self.norm[l]
+            sq, so_, sgu, sd = self.signs[l]
+            ops += [hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1, normw=na, eps=1e-6, hx=self.hx(sq)),
+                    hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0, hx=self.hx(so_)),
+                    hip.StepGemv(G.kSwiglu, E, F, *w("gate", l), 0, 3, *w("up", l), normw=nf, eps=1e-6,
+                                 hx=self.hx(sgu)),
+                    hip.StepGemv(G.kAdd, F, E, *w("down", l), 3, 0, hx=self.hx(sd))]
+        ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 4, normw=self.out_norm, eps=1e-6,
+                                hx=self.hx(self.out_signs)))
+        ops.append(hip.StepArgmax(4, self.tok, self.pos))
+        return ops
+
+    def vecs(self):
+        hip = self.S.hip
+        return [hip.StepVec(E, self.res), hip.StepVec(QKV, self.qkv), hip.StepVec(E, self.att),
+                hip.StepVec(F, self.h), hip.StepVec(V, self.logits)]
+
+    def run(self, st):
+        """The same step as the reference decoder's launches: launch_embed,
+        launch_prep + launch_gemv per GEMV, launch_argmax, launch_pos_add."""
+        hip, S, G = self.S.hip, self.S, self.S.hip.GemvMode
+        N_, K_, _, co, so = S.mats[("embed", self.layers)]
+        base = S.arena.data_ptr()
+        hip.launch_embed(base + co, base + so, self.tok, 1, E, self.hx(self.emb_signs), self.res, st)
+        prep = lambda x, K, normw, signs: hip.launch_prep(x, K, 1, K, normw, 1e-6 if normw is not None else 0.0,
+                                                          self.hx(signs), None, 0, self.act, st)
+        for l in range(self.layers):
+            na, nf = self.norm[l]
+            sq, so_, sgu, sd = self.signs[l]
+            prep(self.res, E, na, sq)
+            hip.launch_gemv([S.seg("qkv", l, self.qkv, QKV)], E, 1, self.act, G.kStore, st)
+            prep(self.att, E, None, so_)
+            hip.launch_gemv([S.seg("o", l, self.res, E)], E, 1, self.act, G.kAdd, st)
+            prep(self.res, E, nf, sgu)
+            hip.launch_gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, 1, self.act, G.kSwiglu, st)
+            prep(self.h, F, None, sd)
+            hip.launch_gemv([S.seg("down", l, self.res, E)], F, 1, self.act, G.kAdd, st)
+        prep(self.res, E, self.out_norm, self.out_signs)
+        hip.launch_gemv([S.seg("output", self.layers, self.logits, V)], E, 1, self.act, G.kStore, st)
+        hip.launch_argmax(self.logits, V, self.part, self.tok, st)
+        hip.launch_pos_add(self.pos, 1, st)
+
+
+def run_token(S: Setup, hip, torch, layers, steps, warmup):
+    """The whole decode step: one step-program launch per token, checked
+    bit-exact against the op-by-op launches (vectors, token, position), then
+    both timed over `steps` tokens (each decoding the previous pick)."""
+    import numpy as np
+    T = Token(S, layers)
+    t0 = time.time()
+    prog = hip.StepProgram(T.vecs(), T.ops())
+    log(f"whole-token program built in {time.time() - t0:.2f} s")
+    try:
+        outs = []
+        for run in (T.run, lambda st: prog.launch(st)):
+            T.reset()
+            torch.cuda.synchronize()
+            run(torch.cuda.current_stream().cuda_stream)
+            torch.cuda.synchronize()
+            outs.append([t.cpu().numpy().copy() for t in (T.res, T.qkv, T.h, T.logits, T.tok, T.pos)])
+        if prog.error():
+            raise SystemExit("whole-token program reported a timeout")
+        for name, a, b in zip(("res", "qkv", "h", "logits", "token", "pos"), *outs):
+            if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
+                raise SystemExit(f"whole-token program != op-by-op launches ({name})")
+        if not np.isfinite(outs[0][3]).all():
+            raise SystemExit("whole-token logits are not finite")
+        log(f"whole-token program vs op-by-op launches: bit-exact (token {int(outs[0][4][0])})")
+        T.reset()
+        ms = time_program(hip, torch, prog, steps, warmup)
+    finally:
+        prog.close()
+    T.reset()
+    gms = time_graph(hip, torch, T.run, steps, warmup)
+    gbs = T.total_bytes / (ms * 1e-3) / 1e9
+    log(f"whole token: step program {ms:.4f} ms ({1e3 / ms:.1f} tok/s, {gbs:.1f} GB/s), "
+        f"op-by-op graph {gms:.4f} ms ({1e3 / gms:.1f} tok/s)")
+    return {
+        "workload": f"whole decode step of the 27B shapes at batch 1: embedding lookup (inverse FWHT 1024 + signs), "
+                    f"{layers} x (QKV, o, gate+up swiglu, down) each with launch_prep's RMSNorm / FWHT 1024 / signs, "
+                    "output 5120->248320 with RMSNorm + FWHT, greedy pick, position counter; each token decodes "
+                    "the previous pick",
+        "ms_per_token": round(ms, 4), "tok_s": round(1e3 / ms, 2), "bytes_per_token": T.total_bytes,
+        "graph_ms_per_token": round(gms, 4), "graph_tok_s": round(1e3 / gms, 2),
+        "kernels_per_token": {"step": 1, "graph": 2 + 2 * (4 * layers + 1) + 2},
+        "verified": "step program bit-exact vs the op-by-op launches (vectors, token, position)",
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "step_kernel (the whole token, one launch)", "bytes_per_launch": T.total_bytes,
+                     "avg_launch_us": round(ms * 1e3, 3)},
+    }
+
+
+def kind_timings(step, layers, steps, fused=False, b3=False):
+    """Per-kind GEMV launch times: a graph of one launch per layer (distinct
+    weights, far beyond the 256 MB MALL) -> the average per launch."""
+    hip, torch = step.S.hip, step.S.torch
+    kinds = ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else [])
+    per = {}
+    launch = step.kind_launch_b3 if b3 else (lambda kind, l, st: step.kind_launch(kind, l, st, fused))
+    table = step.kind_bytes_b3 if b3 else step.kind_bytes
+    for kind in kinds:
+        reps = 1 if kind == "output" else layers
+        fn = (lambda st, kind=kind: launch(kind, 0, st)) if kind == "output" else \
+             (lambda st, kind=kind: [launch(kind, l, st) for l in range(layers)])
+        kms = time_graph(hip, torch, fn, max(3, steps // 2), 1)
+        avg_us = kms * 1e3 / reps
+        b = table[kind]
+        per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
+                     "launches_per_step": 1 if kind == "output" else layers}
+    return per
+
+
+def gemm_roofline(step, per, traffic_tab=None, workload="batched"):
+    """The dominant GEMV/GEMM kind of a batched step and its roofline (HBM
+    below 33 rows, int8 MFMA above)."""
+    dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
+    d = per[dom]
+    if step.M <= 32:
+        tr = (traffic_tab or {}).get(f"batched{step.M}/{dom}")
+        kern = "gemv_dot4_kernel" if step.M < 3 else "gemm_ks_kernel"
+        return dom, {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
+                     "traffic_source": tr["source"] if tr else None, "kernel": f"{dom} GEMM ({kern})",
+                     "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
+    K_ = F if dom == "down" else E
+    N_ = {"qkv": QKV, "o": E, "gateup": 2 * F, "down": E}[dom]
+    tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
+    return dom, {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
+                 "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
+                 "kernel": f"{dom} GEMM (gemm_pf2_kernel, int8 ops)", "ops_per_launch": 2 * step.M * N_ * K_,
+                 "avg_launch_us": d["avg_us"]}
+
+
+def run_batched_sub(S: Setup, M, layers, steps, warmup, traffic_tab):
+    """Batched decode (M <= 32) or prefill (M = 512) on the first `layers`
+    layers of the sweep's weights: the graph of quantize + GEMM launches, and
+    the dominant kind's roofline."""
+    step = Step(S, M, layers, with_output=False)
+    hip, torch = S.hip, S.torch
+    ms = time_graph(hip, torch, step.run, steps, warmup)
+    per = kind_timings(step, layers, steps)
+    dom, roof = gemm_roofline(step, per, traffic_tab)
+    log(f"M={M}: {ms:.4f} ms per {layers}-layer step; dominant {dom} {per[dom]['avg_us']} us, "
+        f"{roof['achieved']} {roof['unit']} ({100 * roof['frac']:.1f} %)")
+    return {"workload": (f"batched decode, M={M}, " if M <= 32 else f"prefill, M={M}, ") +
+                        f"{layers} layers of the 27B shapes, graph of quantize + GEMM launches",
+            "batch": M, "ms_per_step": round(ms, 4), "bytes_per_step": step.total_bytes,
+            "GBs": round(step.total_bytes / (ms * 1e-3) / 1e9, 1), "kinds": per, "roofline": roof}
 
 
 def time_graph(hip, torch, fn, reps, warmup):
@@ -653,7 +875,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill", "load"])
+    ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill", "load", "token"])
+    ap.add_argument("--no-subs", action="store_true",
+                    help="sweep: skip the sub-results (whole token, config 1, batched M=8, prefill M=512)")
     ap.add_argument("--batch", type=int, default=0, help="M for --workload batched (default 4,8,16,32 sweep)")
     ap.add_argument("--layers", type=int, default=LAYERS)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
@@ -702,11 +926,28 @@ def main():
         run_load(args, hip, torch)
         return
 
-    layers = args.layers if args.workload == "sweep" else (1 if args.workload == "layer" else 8)
+    layers = args.layers if args.workload in ("sweep", "token") else (1 if args.workload == "layer" else 8)
     t0 = time.time()
     with_b3 = (args.engine == "auto" if args.b3 is None else args.b3) and args.workload in ("sweep", "layer")
-    S = Setup(hip, torch, layers, keep_src=with_b3)
+    subs_on = args.workload == "sweep" and not args.no_subs
+    S = Setup(hip, torch, layers, keep_src=with_b3, with_embed=subs_on or args.workload == "token")
     log(f"weights generated + repacked: {S.arena_bytes / 1e9:.3f} GB arena in {time.time() - t0:.2f} s")
+    try:
+        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
+            traffic_tab = json.load(f)
+    except (OSError, ValueError):
+        traffic_tab = {}
+
+    if args.workload == "token":
+        tok = run_token(S, hip, torch, layers, args.steps, args.warmup)
+        out = {"metric": "whole-token decode step at batch 1 (tok/s)", "value": tok["tok_s"], "unit": "tok/s",
+               "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": tok["ms_per_token"],
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+               "data": "synthetic (seeded ternary weights, norm weights N(1,0.1), random signs)",
+               "config": {"workload": tok["workload"], "batch": 1, "parallelism": "single GPU"},
+               "roofline": tok["roofline"], "whole_token": tok, "cpu_baseline": None}
+        print(json.dumps(out))
+        return
 
     if args.workload == "sweep":
         step = Step(S, 1, layers)
@@ -786,25 +1027,17 @@ def main():
 
     # Per-kind GEMV timing of the op-by-op path: a graph of one launch per
     # layer (distinct weights) -> average per launch.
-    kinds = ["qkv", "o", "gateup", "down"] + (["output"] if step.with_output else [])
     per = {}
     fk = engine == "chain"
     if not args.no_kinds or engine != "step":
-        for kind in kinds:
-            reps = 1 if kind == "output" else layers
-            fn = (lambda st, kind=kind: step.kind_launch(kind, 0, st, fk)) if kind == "output" else \
-                 (lambda st, kind=kind: [step.kind_launch(kind, l, st, fk) for l in range(layers)])
-            kms = time_graph(hip, torch, fn, max(3, args.steps // 2), 1)
-            avg_us = kms * 1e3 / reps
-            b = step.kind_bytes[kind]
-            per[kind] = {"avg_us": round(avg_us, 3), "bytes": b, "GBs": round(b / (avg_us * 1e-6) / 1e9, 1),
-                         "launches_per_step": 1 if kind == "output" else layers}
-            log(f"  op-by-op {kind}: {avg_us:.3f} us/launch, {per[kind]['GBs']} GB/s")
-    # The kernels either side of the GEMV chain (not part of the sweep's
-    # value): the embedding lookup of one token from a packed table of the
-    # output projection's shape (V x 5120, with the inverse transform at
-    # block 1024 + signs), the greedy pick over V logits (two launches) and
-    # the position counter; graphs of 64 launches each, per-launch average.
+        per = kind_timings(step, layers, args.steps, fused=fk)
+        for kind, d in per.items():
+            log(f"  op-by-op {kind}: {d['avg_us']:.3f} us/launch, {d['GBs']} GB/s")
+    # The kernels either side of the GEMV chain, as separate launches (the
+    # whole-token sub-result runs them inside the step program): the
+    # embedding lookup of one token from the packed V x 5120 table (inverse
+    # transform at block 1024 + signs), the greedy pick over V logits (two
+    # launches) and the position counter; graphs of 64 launches each.
     ends = None
     if step.with_output and args.workload == "sweep":
         N_, K_, _, co, so = S.mats[("output", layers)]
@@ -820,6 +1053,7 @@ def main():
         fns = {
             "embed": lambda st: [hip.launch_embed(base + co, base + so, tp + 4 * i, 1, E, inv, xe, st) for i in range(64)],
             "argmax": lambda st: [hip.launch_argmax(step.logits, V, part, tok_out, st) for _ in range(64)],
+            "argmax_noalloc": lambda st: [hip.launch_argmax_noalloc(step.logits, V, tok_out, st) for _ in range(64)],
             "pos_add": lambda st: [hip.launch_pos_add(pos, 1, st) for _ in range(64)],
         }
         ends = {}
@@ -834,11 +1068,6 @@ def main():
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3
     # FETCH_SIZE / WRITE_SIZE runs (profiles/hbm_traffic.json), when they
     # cover this engine's dominant kernel; counters cannot be read live.
-    try:
-        with open(os.path.join(ROOT, "profiles", "hbm_traffic.json")) as f:
-            traffic_tab = json.load(f)
-    except (OSError, ValueError):
-        traffic_tab = {}
     if engine == "step":
         tr = traffic_tab.get("step/step_kernel") if step.M == 1 and args.workload == "sweep" and \
             layers == LAYERS else None
@@ -847,29 +1076,37 @@ def main():
                 "traffic_source": tr["source"] if tr else None,
                 "kernel": "step_kernel (the whole GEMV chain, one launch per step)",
                 "bytes_per_launch": step.total_bytes, "avg_launch_us": round(ms * 1e3, 3)}
-    else:
+    elif step.M == 1:
         dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
         d = per[dom]
-        if step.M <= 32:
-            if step.M == 1 and args.workload == "sweep":
-                tr = traffic_tab.get(f"{engine}/{dom}")
-            elif args.workload == "batched" and not args.mfma_min_m:
-                tr = traffic_tab.get(f"batched{step.M}/{dom}")  # measured at the default crossover
-            else:
-                tr = None
-            roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                    "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
-                    "traffic_source": tr["source"] if tr else None,
-                    "kernel": f"{dom} GEMV ({'gemv_dot4_kernel' if step.M < (args.mfma_min_m or 3) else 'gemm_ks_kernel'}"
-                              f"{', quantizes fused in' if fk else ''})",
-                    "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
-        else:
-            K_ = F if dom == "down" else E
-            N_ = {"qkv": QKV, "o": E, "gateup": 2 * F, "down": E}[dom]
-            tops = 2 * step.M * N_ * K_ / (d["avg_us"] * 1e-6) / 1e12
-            roof = {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS, "unit": "TFLOP/s",
-                    "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None,
-                    "kernel": f"{dom} GEMM (gemm_pf2_kernel, int8 ops)", "avg_launch_us": d["avg_us"]}
+        tr = traffic_tab.get(f"{engine}/{dom}") if args.workload == "sweep" else None
+        roof = {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
+                "traffic_source": tr["source"] if tr else None,
+                "kernel": f"{dom} GEMV (gemv_dot4_kernel{', quantizes fused in' if fk else ''})",
+                "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
+    else:
+        _, roof = gemm_roofline(step, per, traffic_tab if not args.mfma_min_m else {})
+
+    # Sub-results of the default run, each with its own roofline: the whole
+    # decode step in one launch; config 1 (the 5120 -> 5120 GEMV, 64 distinct
+    # matrices rotated past the MALL, from the per-kind timings); config 3
+    # (batched decode M = 8) and config 4 (prefill M = 512) on 8 layers.
+    subs = None
+    if subs_on:
+        subs = {"whole_token": run_token(S, hip, torch, layers, args.steps, args.warmup)}
+        if "o" in per:
+            d = per["o"]
+            subs["config1_gemv_5120x5120"] = {
+                "workload": "GEMV M=1, K=5120 -> N=5120 (the o projection of 64 distinct layers, 445 MB rotated "
+                            "past the 256 MB MALL), Q8 input quantized by its own launch",
+                "avg_us": d["avg_us"], "bytes_per_launch": d["bytes"], "GBs": d["GBs"],
+                "roofline": {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                             "kernel": "gemv_dot4_kernel (o projection)", "bytes_per_launch": d["bytes"],
+                             "avg_launch_us": d["avg_us"]}}
+        subs["config3_batched_m8"] = run_batched_sub(S, 8, 8, args.steps, args.warmup, traffic_tab)
+        subs["config4_prefill_m512"] = run_batched_sub(S, 512, 8, max(5, args.steps // 2), 2, traffic_tab)
 
     out = {
         "metric": METRIC,
@@ -904,6 +1141,7 @@ def main():
         "verified": {"vs_graph_engine_bit_exact": verified} if verified else None,
         "engines_ms": {k: round(v, 4) for k, v in engine_ms.items()},
         "gemv_kinds": per,
+        "sub_results": subs,
         "decode_step_ends": ends,
         "ptq1_0_direct": b3,
         "device": {"name": info["name"], "arch": info["gcn_arch"], "cus": info["cu_count"]},
