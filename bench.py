@@ -336,10 +336,14 @@ class Token:
 
     BLOCK = 1024
 
-    def __init__(self, S: Setup, layers, seed=1):
+    def __init__(self, S: Setup, layers, seed=1, prep="full"):
+        """prep: "full" (the decoder's RMSNorms and transforms), or for
+        measurement "hx" (transforms only), "norm" (norms only), "none"."""
         import numpy as np
         hip, torch = S.hip, S.torch
         self.S, self.layers = S, layers
+        self.use_norm = prep in ("full", "norm")
+        self.use_hx = prep in ("full", "hx")
         rng = np.random.default_rng(seed)
         dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
         sg = lambda n: dev(np.where(rng.random(n) < 0.5, -1.0, 1.0).astype(np.float32))
@@ -373,7 +377,10 @@ class Token:
         self.pos.zero_()
 
     def hx(self, signs):
-        return self.S.hip.Hx(block=self.BLOCK, signs=signs)
+        return self.S.hip.Hx(block=self.BLOCK, signs=signs) if self.use_hx else None
+
+    def nw(self, w):
+        return w if self.use_norm else None
 
     def ops(self):
         """The step program's ops. Vector slots: 0 residual, 1 qkv, 2
@@ -389,13 +396,13 @@ class Token:
         for l in range(self.layers):
             na, nf = self.norm[l]
             sq, so_, sgu, sd = self.signs[l]
-            ops += [hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1, normw=na, eps=1e-6, hx=self.hx(sq)),
+            ops += [hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1, normw=self.nw(na), eps=1e-6, hx=self.hx(sq)),
                     hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0, hx=self.hx(so_)),
-                    hip.StepGemv(G.kSwiglu, E, F, *w("gate", l), 0, 3, *w("up", l), normw=nf, eps=1e-6,
+                    hip.StepGemv(G.kSwiglu, E, F, *w("gate", l), 0, 3, *w("up", l), normw=self.nw(nf), eps=1e-6,
                                  hx=self.hx(sgu)),
                     hip.StepGemv(G.kAdd, F, E, *w("down", l), 3, 0, hx=self.hx(sd))]
-        ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 4, normw=self.out_norm, eps=1e-6,
-                                hx=self.hx(self.out_signs)))
+        ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 4, normw=self.nw(self.out_norm),
+                                eps=1e-6, hx=self.hx(self.out_signs)))
         ops.append(hip.StepArgmax(4, self.tok, self.pos))
         return ops
 
@@ -416,26 +423,26 @@ class Token:
         for l in range(self.layers):
             na, nf = self.norm[l]
             sq, so_, sgu, sd = self.signs[l]
-            prep(self.res, E, na, sq)
+            prep(self.res, E, self.nw(na), sq)
             hip.launch_gemv([S.seg("qkv", l, self.qkv, QKV)], E, 1, self.act, G.kStore, st)
             prep(self.att, E, None, so_)
             hip.launch_gemv([S.seg("o", l, self.res, E)], E, 1, self.act, G.kAdd, st)
-            prep(self.res, E, nf, sgu)
+            prep(self.res, E, self.nw(nf), sgu)
             hip.launch_gemv([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, 1, self.act, G.kSwiglu, st)
             prep(self.h, F, None, sd)
             hip.launch_gemv([S.seg("down", l, self.res, E)], F, 1, self.act, G.kAdd, st)
-        prep(self.res, E, self.out_norm, self.out_signs)
+        prep(self.res, E, self.nw(self.out_norm), self.out_signs)
         hip.launch_gemv([S.seg("output", self.layers, self.logits, V)], E, 1, self.act, G.kStore, st)
         hip.launch_argmax(self.logits, V, self.part, self.tok, st)
         hip.launch_pos_add(self.pos, 1, st)
 
 
-def run_token(S: Setup, hip, torch, layers, steps, warmup):
+def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full"):
     """The whole decode step: one step-program launch per token, checked
     bit-exact against the op-by-op launches (vectors, token, position), then
     both timed over `steps` tokens (each decoding the previous pick)."""
     import numpy as np
-    T = Token(S, layers)
+    T = Token(S, layers, prep=prep)
     t0 = time.time()
     prog = hip.StepProgram(T.vecs(), T.ops())
     log(f"whole-token program built in {time.time() - t0:.2f} s")
@@ -876,6 +883,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="sweep", choices=["sweep", "layer", "batched", "prefill", "load", "token"])
+    ap.add_argument("--token-prep", default="full", choices=["full", "hx", "norm", "none"],
+                    help="--workload token: the GEMV input preps (the decoder's norms and transforms, or a part)")
     ap.add_argument("--no-subs", action="store_true",
                     help="sweep: skip the sub-results (whole token, config 1, batched M=8, prefill M=512)")
     ap.add_argument("--batch", type=int, default=0, help="M for --workload batched (default 4,8,16,32 sweep)")
@@ -939,7 +948,7 @@ def main():
         traffic_tab = {}
 
     if args.workload == "token":
-        tok = run_token(S, hip, torch, layers, args.steps, args.warmup)
+        tok = run_token(S, hip, torch, layers, args.steps, args.warmup, args.token_prep)
         out = {"metric": "whole-token decode step at batch 1 (tok/s)", "value": tok["tok_s"], "unit": "tok/s",
                "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": tok["ms_per_token"],
                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",

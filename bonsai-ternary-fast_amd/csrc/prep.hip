@@ -16,12 +16,13 @@
 //    include/btf/packed.hpp:117-134: d = fp16_rn(amax/127) (IEEE division),
 //    q = rint(x * (127/amax)) with ties to even, s = sum q. An all-zero block
 //    gets d = +-0 with the sign of its last element, as the CPU loop does.
-//  * prep_slices_kernel<NORM, PERM>: the full transform, a wave per
-//    1024-value slice in registers (slice.h): the FWHT runs in the CPU's
-//    stage order, so without the norm the result is bit-exact; the RMSNorm's
-//    double sum of squares is taken in a fixed canonical order (per 32-value
-//    block, then over the blocks), so its last bit can differ from the CPU's
-//    sequential sum (the reference's own GPU kernel differs likewise).
+//  * prep_slice_kernel<NORM, PERM, VEC>: the full transform, a wave per
+//    (1024-value slice, row) in registers (slice.h): the FWHT runs in the
+//    CPU's stage order, so without the norm the result is bit-exact; the
+//    RMSNorm's double sum of squares is taken in a fixed canonical order (per
+//    32-value block, then over the blocks), so its last bit can differ from
+//    the CPU's sequential sum (the reference's own GPU kernel differs
+//    likewise).
 #include <cmath>
 
 #include "../../include/btf/hip_abi.h"
@@ -34,7 +35,6 @@ namespace btfhip {
 namespace {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr size_t kMaxPrepLds = 64 * 1024;  // block sums of squares of one row (normed prep)
 
 // Quantize 8 consecutive values of one Q8 block held by this lane; the 4
 // lanes of a DPP quad hold the block. Returns the two packed q words; d and s
@@ -103,18 +103,18 @@ __global__ void __launch_bounds__(256) q8_kernel(const float* __restrict__ x, in
 }
 
 // ---- full prep ----
-// One workgroup per row, W waves (W = min(16, slices)); wave w takes the
-// 1024-value slices w, w + W, ... of the row in registers (slice.h: lane l
-// holds values 16 l .. 16 l + 15). With the norm, the waves first write the
-// canonical sum of squares of every 32-value block of the row into LDS, and
-// every wave forms the row's scale from them in one fixed order (so the
-// step program, which gathers the same block sums from its producers, gets
-// the same scale bit for bit). Then per slice: gather through the perm,
-// (x * scale) * w, the normed row to xn_out, * signs, the blockwise FWHT in
-// registers, * 1/sqrt(block), the Q8 of each lane pair's block.
+// One wave per (1024-value slice, row), every one independent: with the
+// norm, the wave first forms the row's RMSNorm scale itself -- lane l sums
+// the canonical sums of squares of 32-value blocks l, l + 64, ... (128
+// contiguous bytes per lane and block), then the wave sum (slice.h), the
+// order in which the step program sums its producers' block sums, so both
+// get the same scale bit for bit. Then its slice in registers (lane l holds
+// values 16 l .. 16 l + 15): gather through the perm, (x * scale) * w, the
+// normed values to xn_out, * signs, the blockwise FWHT, * 1/sqrt(block), the
+// Q8 of each lane pair's block.
 struct PrepArgs {
   const float* x;
-  int ldx, n, nslices;
+  int ldx, n;
   const float* normw;
   float eps;
   int block, hd, nk, rep;  // rep > 1: tiled -> grouped gather
@@ -127,71 +127,87 @@ struct PrepArgs {
   int32_t* s;
 };
 
-template <bool NORM, bool PERM>
-__global__ void __launch_bounds__(1024) prep_slices_kernel(PrepArgs a) {
-  extern __shared__ double bsum[];  // [n / 32] block sums of squares (NORM)
-  const int m = blockIdx.x, lane = threadIdx.x & 63, wave = threadIdx.x >> 6, W = blockDim.x >> 6;
+// 16 consecutive values of row xr from index c0 (16-byte loads when VEC).
+template <bool VEC>
+__device__ __forceinline__ void load16(const float* xr, int c0, float (&v)[16]) {
+  if (VEC) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const f32x4 t = reinterpret_cast<const f32x4*>(xr + c0)[k];
+      v[4 * k] = t.x;
+      v[4 * k + 1] = t.y;
+      v[4 * k + 2] = t.z;
+      v[4 * k + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = xr[c0 + i];
+  }
+}
+
+template <bool NORM, bool PERM, bool VEC>
+__global__ void __launch_bounds__(64) prep_slice_kernel(PrepArgs a) {
+  const int lane = threadIdx.x, m = blockIdx.y;
   const float* xr = a.x + (size_t)m * a.ldx;
   float scale = 1.0f;
   if (NORM) {
-    for (int sl = wave; sl < a.nslices; sl += W) {
-      const int c0 = sl * kSliceVals + 16 * lane;
-      float v[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = c0 + i < a.n ? xr[c0 + i] : 0.f;
-      const double bs = pair_sumsq(v);
-      if (!(lane & 1) && c0 < a.n) bsum[c0 >> 5] = bs;
-    }
-    __syncthreads();
     double acc = 0.0;
-    for (int i = lane; i < (a.n >> 5); i += 64) acc += bsum[i];
+    for (int b = lane; b < (a.n >> 5); b += 64) {
+      float lo[16], hi[16];
+      load16<VEC>(xr, 32 * b, lo);
+      load16<VEC>(xr, 32 * b + 16, hi);
+      acc += block_sumsq(lo, hi);
+    }
     scale = norm_scale_of(acc, a.n, a.eps);
   }
-  const bool xform = a.block > 0;
-  for (int sl = wave; sl < a.nslices; sl += W) {
-    const int c0 = sl * kSliceVals + 16 * lane;
-    const bool live = c0 < a.n;  // a.n % 32 == 0: a lane pair is all in or all out
-    float v[16];
+  const int c0 = blockIdx.x * kSliceVals + 16 * lane;
+  const bool live = c0 < a.n;  // a.n % 32 == 0: a lane pair is all in or all out
+  float v[16];
+  if (live) {
+    if (PERM) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) v[i] = xr[perm_src(c0 + i, a.hd, a.nk, a.rep)];
+    } else {
+      load16<VEC>(xr, c0, v);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = 0.f;
+  }
+  if (NORM && live)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * a.normw[PERM ? perm_src(c0 + i, a.hd, a.nk, a.rep) : c0 + i];
+  if (a.xn && live) {
+    float* xo = a.xn + (size_t)m * a.ldxn + c0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const int og = c0 + i;
-      const int src = PERM ? perm_src(og, a.hd, a.nk, a.rep) : og;
-      float u = live ? xr[src] : 0.f;
-      if (NORM) u = (u * scale) * (live ? a.normw[src] : 0.f);
-      v[i] = u;
+      float u = xr[c0 + i];
+      if (NORM) u = (u * scale) * a.normw[c0 + i];
+      xo[i] = u;
     }
-    if (a.xn && live) {
-      float* xo = a.xn + (size_t)m * a.ldxn + c0;
+  }
+  if (a.block > 0) {
+    if (a.signs && live)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float u = xr[c0 + i];
-        if (NORM) u = (u * scale) * a.normw[c0 + i];
-        xo[i] = u;
-      }
-    }
-    if (xform) {
-      if (a.signs)
+      for (int i = 0; i < 16; ++i) v[i] = v[i] * a.signs[c0 + i];
+    slice_fwht(v, lane, a.block);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) v[i] = v[i] * (live ? a.signs[c0 + i] : 0.f);
-      slice_fwht(v, lane, a.block);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = v[i] * a.hs;
-    }
-    uint32_t qw[4];
-    float dd;
-    int ss;
-    q8_pair(v, qw, dd, ss);
-    if (live) {
-      uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + (size_t)m * a.n + c0);
-      qp[0] = qw[0];
-      qp[1] = qw[1];
-      qp[2] = qw[2];
-      qp[3] = qw[3];
-      if (!(lane & 1)) {
-        const size_t bi = (size_t)m * (a.n >> 5) + (c0 >> 5);
-        a.d[bi] = dd;
-        a.s[bi] = ss;
-      }
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * a.hs;
+  }
+  uint32_t qw[4];
+  float dd;
+  int ss;
+  q8_pair(v, qw, dd, ss);
+  if (live) {
+    uint32_t* qp = reinterpret_cast<uint32_t*>(a.q + (size_t)m * a.n + c0);
+    qp[0] = qw[0];
+    qp[1] = qw[1];
+    qp[2] = qw[2];
+    qp[3] = qw[3];
+    if (!(lane & 1)) {
+      const size_t bi = (size_t)m * (a.n >> 5) + (c0 >> 5);
+      a.d[bi] = dd;
+      a.s[bi] = ss;
     }
   }
 }
@@ -217,13 +233,10 @@ int prep(const float* x, int ldx, int M, int n, const float* normw, float eps, i
   int span = 1024;
   while (n % span) span >>= 1;
   if (block > 0 && span % block) return fail(BTF_ERR_ARGS, "prep: hadamard block does not divide the span");
-  if (normw && (size_t)(n / 32) * sizeof(double) > kMaxPrepLds)
-    return fail(BTF_ERR_ARGS, "prep: width too large for the normed prep (n <= 262144)");
   PrepArgs p{};
   p.x = x;
   p.ldx = ldx;
   p.n = n;
-  p.nslices = (n + kSliceVals - 1) / kSliceVals;
   p.normw = normw;
   p.eps = eps;
   p.block = block > 0 ? block : 0;
@@ -238,21 +251,25 @@ int prep(const float* x, int ldx, int M, int n, const float* normw, float eps, i
   p.q = q;
   p.d = d;
   p.s = s;
-  const int waves = p.nslices < 16 ? p.nslices : 16;
-  const size_t lds = normw ? (size_t)(n / 32) * sizeof(double) : 0;
-  const dim3 grid(M), blk(64 * waves);
+  const bool vec = ((reinterpret_cast<uintptr_t>(x) & 15) == 0) && (ldx % 4 == 0);
+  const dim3 grid((n + kSliceVals - 1) / kSliceVals, M), blk(64);
+#define BTF_PREP_LAUNCH(NORM, PERM, VEC) \
+  hipLaunchKernelGGL((prep_slice_kernel<NORM, PERM, VEC>), grid, blk, 0, st, p)
   if (normw) {
-    if (perm)
-      hipLaunchKernelGGL((prep_slices_kernel<true, true>), grid, blk, lds, st, p);
-    else
-      hipLaunchKernelGGL((prep_slices_kernel<true, false>), grid, blk, lds, st, p);
+    if (perm) {
+      if (vec) BTF_PREP_LAUNCH(true, true, true); else BTF_PREP_LAUNCH(true, true, false);
+    } else {
+      if (vec) BTF_PREP_LAUNCH(true, false, true); else BTF_PREP_LAUNCH(true, false, false);
+    }
   } else {
-    if (perm)
-      hipLaunchKernelGGL((prep_slices_kernel<false, true>), grid, blk, 0, st, p);
-    else
-      hipLaunchKernelGGL((prep_slices_kernel<false, false>), grid, blk, 0, st, p);
+    if (perm) {
+      if (vec) BTF_PREP_LAUNCH(false, true, true); else BTF_PREP_LAUNCH(false, true, false);
+    } else {
+      if (vec) BTF_PREP_LAUNCH(false, false, true); else BTF_PREP_LAUNCH(false, false, false);
+    }
   }
-  return launch_status("prep_slices_kernel");
+#undef BTF_PREP_LAUNCH
+  return launch_status("prep_slice_kernel");
 }
 
 }  // namespace btfhip

@@ -108,6 +108,25 @@ __device__ __forceinline__ void slice_fwht(float (&v)[16], int lane, int block) 
   if (block > 512) xstage<32>(v, lane);
 }
 
+// The same butterflies for a slice held strided: lane l holds values
+// l + 64 i (i = 0..15), so loads of consecutive values are coalesced across
+// the wave. Stages len = 1..32 pair lane l with lane l ^ len, stages
+// len = 64..512 pair entries i and i ^ (len / 64) inside the lane; the order
+// of the stages and the arithmetic of each butterfly are the CPU's.
+__device__ __forceinline__ void slice_fwht_strided(float (&v)[16], int lane, int block) {
+  asm volatile("" : "+s"(block));
+  if (block > 1) xstage<1>(v, lane);
+  if (block > 2) xstage<2>(v, lane);
+  if (block > 4) xstage<4>(v, lane);
+  if (block > 8) xstage<8>(v, lane);
+  if (block > 16) xstage<16>(v, lane);
+  if (block > 32) xstage<32>(v, lane);
+  if (block > 64) istage<1>(v);
+  if (block > 128) istage<2>(v);
+  if (block > 256) istage<4>(v);
+  if (block > 512) istage<8>(v);
+}
+
 // Q8_0 of the 32-value block held by a lane pair (l, l ^ 1): the q bytes of
 // this lane's 16 values as 4 little-endian words (word k = values 4k..4k+3),
 // and the block's d and s in both lanes. Arithmetic of the q8 kernel
@@ -158,6 +177,29 @@ __device__ __forceinline__ double pair_sumsq(const float (&v)[16]) {
   t[1] = t[2] + t[3];
   t[0] = t[0] + t[1];
   return t[0] + lane_xor_d<1>(t[0]);
+}
+
+// The same canonical sum of squares of a 32-value block held in one lane
+// (lo = values 0..15, hi = values 16..31).
+__device__ __forceinline__ double block_sumsq(const float (&lo)[16], const float (&hi)[16]) {
+  double t[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const double a = (double)lo[2 * i], b = (double)lo[2 * i + 1];
+    const double c = (double)hi[2 * i], d = (double)hi[2 * i + 1];
+    const double sa = a * a, sb = b * b, sc = c * c, sd = d * d;
+    t[i] = sa + sb;
+    t[8 + i] = sc + sd;
+  }
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[8 * h + i] = t[8 * h + 2 * i] + t[8 * h + 2 * i + 1];
+    t[8 * h] = t[8 * h] + t[8 * h + 1];
+    t[8 * h + 1] = t[8 * h + 2] + t[8 * h + 3];
+    t[8 * h] = t[8 * h] + t[8 * h + 1];
+  }
+  return t[0] + t[8];
 }
 
 // Sum over the wave of one double per lane, every lane getting the total:

@@ -43,6 +43,7 @@
 #include <climits>
 #include <cmath>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 #include "../../include/btf/hip_abi.h"
@@ -114,10 +115,11 @@ static_assert(sizeof(OpDev) == 144, "descriptor layout");
 struct PrepDev {
   const float* normw;  // NULL: no RMSNorm
   const float* signs;  // NULL: none
+  const int* runs;     // the tiled -> grouped gather: first source of each 64-value run (NULL: none)
   float eps;
   float hs;            // 1 / sqrtf(block)
   int block;           // 0: no transform
-  int hd, nk, rep;     // rep > 1: tiled -> grouped gather
+  int pad;
 };
 
 // The program's greedy pick: every workgroup publishes the largest key of
@@ -176,8 +178,11 @@ struct Lds {
   uint32_t ucnt[kCW][kMaxUnits];  // per compute wave: items of each local unit of the current op it has done
   uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
   uint64_t argk[kIW];         // per I/O wave: the largest pick key of the rows it published
+  uint32_t sready[2][kMaxK / kSliceVals];  // prep inputs: op index + 1 once slice sl of buffer ob is in LDS
   WorkRec wrec[kRecSlots][kCW];
   OpRec orec[kRecSlots];
+  const PrepDev* preps;  // kernel arguments read where needed (not held in
+  const HeadDev* head;   // scalar registers through the kernel)
   uint32_t epoch;
   uint32_t abort_;
   uint32_t spin_max;
@@ -335,7 +340,8 @@ struct PrepRegs {  // a PrepDev in scalar registers
   const float* normw;
   const float* signs;
   float eps, hs;
-  int block, hd, nk, rep;
+  int block;
+  bool perm;
 };
 __device__ __forceinline__ PrepRegs prep_regs(const PrepDev* preps, int i) {
   const PrepDev& p = preps[i];
@@ -345,9 +351,7 @@ __device__ __forceinline__ PrepRegs prep_regs(const PrepDev* preps, int i) {
   r.eps = __int_as_float(sgpr(__float_as_int(p.eps)));
   r.hs = __int_as_float(sgpr(__float_as_int(p.hs)));
   r.block = sgpr(p.block);
-  r.hd = sgpr(p.hd);
-  r.nk = sgpr(p.nk);
-  r.rep = sgpr(p.rep);
+  r.perm = sgpr_ptr(p.runs) != nullptr;
   return r;
 }
 
@@ -392,20 +396,37 @@ __device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd,
   return norm_scale_of(acc, K, pd.eps);
 }
 
-// Slice sl of a prep GEMV's input into LDS buffer `ob` (Q8 image).
-__device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepRegs& pd, float scale, Lds& L, int lane,
-                                                 Ctl* ctl, uint32_t base_tag, int ob, int sl) {
+// Slice sl of a prep GEMV's input into LDS buffer `ob` (Q8 image). The wave
+// holds the slice strided (slice.h): lane l takes values sl * 1024 + l + 64 i,
+// so every LL load instruction reads 64 consecutive words (512 contiguous
+// bytes); the 32-value Q8 block of entry i is then the half-wave
+// (lane >> 5) at i (the producers' q8_half), and four consecutive lanes
+// pack their q bytes into one word. With the perm, each 64-value run comes
+// from 64 consecutive sources (the step program takes perm_hd % 64 == 0), so
+// the gather costs one uniform source index per run, recomputed at each use
+// (an empty asm keeps the compiler from holding 16 of them in registers).
+template <bool PERM>
+__device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev* preps, int pi, float scale, Lds& L,
+                                                 int lane, Ctl* ctl, uint32_t base_tag, int ob, int sl) {
+  // Each field of the prep is loaded (a scalar load) where it is used: the
+  // pointer passes an empty asm before every use, so no field is held in
+  // scalar registers across the polls.
+  auto P = [&]() {
+    const PrepDev* p = preps + pi;
+    asm volatile("" : "+s"(p));
+    return p;
+  };
   const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
-  const int c0 = sl * kSliceVals + 16 * lane;
-  // the lane's 16 values come from 16 consecutive sources (the step program
-  // takes perm_hd % 16 == 0, so a 16-value run never crosses a perm tile);
-  // the geometry passes an empty asm so its division constants are formed
-  // per slice, not held through the caller's loop
-  int hd = pd.hd, nk = pd.nk, rep = pd.rep;
-  asm volatile("" : "+s"(hd), "+s"(nk), "+s"(rep));
-  const int src0 = rep > 1 ? perm_src(c0, hd, nk, rep) : c0;
-  auto src = [&](int i) { return src0 + i; };
+  const int c = sl * kSliceVals;
+  // word index of entry i of this lane: with the perm, run i's first source
+  // from the program's table (a scalar load at each use), plus the lane
+  auto src = [&](int i) {
+    if constexpr (PERM)
+      return P()->runs[(c >> 6) + i] + lane;  // (no readfirstlane: the reload below is under a lane mask)
+    else
+      return c + 64 * i + lane;
+  };
   uint64_t w[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) w[i] = ll_load(in + src(i));
@@ -416,34 +437,43 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepRegs
     for (int i = 0; i < 16; ++i) pending |= ((uint32_t)(w[i] >> 32) != tin) ? (1u << i) : 0u;
     if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
     if (!poll_step(spins, L, ctl)) break;
-#pragma unroll
+    // (no unroll pragma: the compiler unrolls this loop by itself -- w[]
+    // lives in registers, the resource test would see scratch otherwise --
+    // and an explicit request only draws a warning for a peeled copy)
     for (int i = 0; i < 16; ++i)
       if (pending & (1u << i)) w[i] = ll_load(in + src(i));
   }
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = __uint_as_float((uint32_t)w[i]);
-  if (pd.normw)
+  if (const float* normw = sgpr_ptr(P()->normw))
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * pd.normw[src(i)];
-  if (pd.block > 0) {
-    if (pd.signs)
+    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * normw[src(i)];
+  if (const int block = sgpr(P()->block); block > 0) {
+    if (const float* signs = sgpr_ptr(P()->signs))
 #pragma unroll
-      for (int i = 0; i < 16; ++i) v[i] = v[i] * pd.signs[c0 + i];
-    slice_fwht(v, lane, pd.block);
+      for (int i = 0; i < 16; ++i) v[i] = v[i] * signs[c + 64 * i + lane];
+    slice_fwht_strided(v, lane, block);
+    const float hs = __int_as_float(sgpr(__float_as_int(P()->hs)));
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = v[i] * pd.hs;
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * hs;
   }
-  uint32_t qw[4];
-  float d;
-  int s;
-  q8_pair(v, qw, d, s);
-  uint32_t* dst = &L.act[ob][(c0 >> 5) * kWordsPerBlock];
-  const int h = lane & 1;  // first or second half of the block's 8 q words
+  int lq = lane;
+  asm volatile("" : "+v"(lq));  // lane tests formed here, not held from the kernel's start
+  const int j = lq & 31, h = lq >> 5;
 #pragma unroll
-  for (int k = 0; k < 4; ++k) dst[4 * h + k] = qw[k];
-  dst[8] = __float_as_uint(d);  // both lanes of the pair store the block's d and s (the same values)
-  dst[9] = (uint32_t)s;
+  for (int i = 0; i < 16; ++i) {
+    float d;
+    int s;
+    const int q = q8_half(v[i], d, s);
+    const uint32_t b = (uint32_t)(q & 0xff) << (8 * (j & 3));
+    uint32_t wq = b | (uint32_t)dpp_i<0xB1>((int)b);  // quad_perm(1,0,3,2)
+    wq |= (uint32_t)dpp_i<0x4E>((int)wq);             // quad_perm(2,3,0,1)
+    uint32_t* dst = &L.act[ob][(sl * 32 + 2 * i + h) * kWordsPerBlock];
+    if ((j & 3) == 0) dst[j >> 2] = wq;
+    if (j == 0) dst[8] = __float_as_uint(d);
+    if (j == 1) dst[9] = (uint32_t)s;
+  }
 }
 
 // ---------------------------------------------------------------- compute waves
@@ -782,7 +812,7 @@ __device__ __forceinline__ bool sum_lanes(int l16) {
 // per-batch bookkeeping (addresses, partial-sum slots, the unit's count, the
 // activation reload at a new slice) is uniform and done once per batch.
 __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
-                                              uint32_t base_tag, const PrepDev* preps) {
+                                              uint32_t base_tag) {
   const int l16 = lane & 15, grp = lane >> 4;
   const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
   const bool sum_lane = sum_lanes(l16);
@@ -802,6 +832,33 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
   for (int opi = first;;) {
     const int ob = opi & 1;  // LDS buffers of this op
     {
+    // An input with a prep: the op's slices are shared out over the compute
+    // waves (wave w takes slices w, w + kCW, ...), each slice prepped once
+    // per workgroup into the LDS image and flagged -- by every wave with a
+    // share, whether or not it has items of the op; below, every wave with
+    // items waits for the flags of the slices its items read.
+    const int pi = sgpr(L.opd[opi].prep);
+    if (pi >= 0 && wave < sgpr(L.opd[opi].K) / kSliceVals) {
+      float scale = 1.0f;
+      bool perm;
+      {
+        const PrepRegs pd = prep_regs(sgpr_ptr(L.preps), pi);
+        perm = pd.perm;
+        if (pd.normw) scale = prep_scale(L.opd[opi], pd, L, lane, ctl, base_tag);
+      }
+      auto mine = [&](auto pm) {
+        for (int sl = wave; sl < sgpr(L.opd[opi].K) / kSliceVals; sl += kCW) {
+          fetch_prep_slice<decltype(pm)::value>(L.opd[opi], sgpr_ptr(L.preps), sgpr(L.opd[opi].prep), scale, L,
+                                                lane, ctl, base_tag, ob, sl);
+          asm volatile("" ::: "memory");  // the image words before the flag (LDS ops of a wave complete in order)
+          __hip_atomic_store(&L.sready[ob][sl], (uint32_t)opi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        }
+      };
+      if (perm)
+        mine(std::true_type{});
+      else
+        mine(std::false_type{});
+    }
     const OpWork cur = op_work(L, wave, opi);
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
@@ -821,20 +878,23 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
       } else {
         int a0, a1, b0w, b1w;
         input_words(cur, a0, a1, b0w, b1w);
-        const int pi = sgpr(L.opd[cur.i].prep);
-        if (pi >= 0) {  // the input's prep, slice by slice (the ranges are whole slices)
-          const PrepRegs pd = prep_regs(preps, pi);
-          const float scale = pd.normw ? prep_scale(L.opd[cur.i], pd, L, lane, ctl, base_tag) : 1.0f;
+        if (pi >= 0) {  // wait for the prepped slices this wave's items read
           constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
-          for (int sl = a0 / kWS; sl < a1 / kWS; ++sl)
-            fetch_prep_slice(L.opd[cur.i], pd, scale, L, lane, ctl, base_tag, ob, sl);
-          for (int sl = b0w / kWS; sl < b1w / kWS; ++sl)
-            fetch_prep_slice(L.opd[cur.i], pd, scale, L, lane, ctl, base_tag, ob, sl);
+          const int s1 = a0 / kWS, n1 = a1 / kWS - s1, s2 = b0w / kWS, n = n1 + b1w / kWS - s2;
+          for (int k = 0; k < n; ++k) {
+            const int sl = k < n1 ? s1 + k : s2 + (k - n1);
+            uint32_t spins = 0;
+            while (__hip_atomic_load(&L.sready[ob][sl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) !=
+                   (uint32_t)cur.i + 1) {
+              if (!poll_step(spins, L, ctl)) break;
+            }
+          }
+          asm volatile("" ::: "memory");
         } else {
           fetch_words(L.opd[cur.i], L, lane, ctl, base_tag, ob, a0, a1, b0w, b1w);
+          // the words other lanes of this wave wrote are read below
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         }
-        // the words other lanes of this wave wrote are read below
-        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       }
     }
     }
@@ -1185,7 +1245,7 @@ __device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int 
 // op's input (and publish its pick key), finish the early fetch. Prologue ops
 // (quantize, embedding) run before the first GEMV.
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
-                                         uint32_t base_tag, const PrepDev* preps, const HeadDev* head) {
+                                         uint32_t base_tag) {
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
     const int kind = sgpr(op.kind);
@@ -1194,7 +1254,7 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       continue;
     }
     if (kind == 2) {
-      io_embed(op, prep_regs(preps, sgpr(op.prep)), wg, G, iol, base_tag + sgpr(op.my_tag));
+      io_embed(op, prep_regs(sgpr_ptr(L.preps), sgpr(op.prep)), wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
     const int nx = sgpr(op.next);
@@ -1217,14 +1277,14 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
       const uint64_t k = key_max(L.argk[0], L.argk[1]);
-      uint64_t* dst = sgpr_ptr(head->parts) + 2 * wg;
+      uint64_t* dst = sgpr_ptr(sgpr_ptr(L.head)->parts) + 2 * wg;
       const uint32_t tag = base_tag + sgpr(op.my_tag);
       ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)k);
       ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(k >> 32));
     }
     if (!early_done) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, true, (uint32_t)nx + 1);
   }
-  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(head->present)) io_pick(head, L, G, iol, ctl, base_tag);
+  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(sgpr_ptr(L.head)->present)) io_pick(sgpr_ptr(L.head), L, G, iol, ctl, base_tag);
 }
 
 // ---------------------------------------------------------------- the kernel
@@ -1242,8 +1302,11 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
     for (int k = threadIdx.x; k < nvec; k += kThreads) dst[k] = src[k];
   }
   for (int k = threadIdx.x; k < kCW * kMaxUnits; k += kThreads) (&L.ucnt[0][0])[k] = 0;
+  for (int k = threadIdx.x; k < 2 * (kMaxK / kSliceVals); k += kThreads) (&L.sready[0][0])[k] = 0;
   if (threadIdx.x < kIW) L.early_seq[threadIdx.x] = 0;
   if (threadIdx.x == 0) {
+    L.preps = preps;
+    L.head = head;
     L.epoch = ctl_load(&ctl->epoch);
     const uint32_t sm = ctl_load(&ctl->spin_max);
     L.spin_max = sm ? sm : kSpinMax;
@@ -1260,13 +1323,13 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
   const uint32_t base_tag = L.epoch * (uint32_t)(nops + 1);
 
   if (wave < kCW)
-    compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag, preps);
+    compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
   else {
     // The I/O waves' epilogue of an op is on the chain's critical path while
     // the compute waves already run the next op's dot products on the same
     // SIMDs: their instructions issue first (the waits in between sleep).
     __builtin_amdgcn_s_setprio(3);
-    io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag, preps, head);
+    io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
     __builtin_amdgcn_s_setprio(0);
   }
 
@@ -1338,8 +1401,8 @@ int check_gemv_op(const btf_step_vec* vecs, int nvec, const btf_step_op& o) {
     if (o.hx.block > 0 && o.hx.perm_rep > 1 &&
         (o.hx.perm_hd <= 0 || o.hx.perm_nk <= 0 || (int64_t)o.hx.perm_hd * o.hx.perm_nk * o.hx.perm_rep != g.K))
       return fail(BTF_ERR_ARGS, "step: hadamard perm geometry");
-    if (o.hx.block > 0 && o.hx.perm_rep > 1 && o.hx.perm_hd % 16)
-      return fail(BTF_ERR_ARGS, "step: the perm's tile (perm_hd) must be a multiple of 16");
+    if (o.hx.block > 0 && o.hx.perm_rep > 1 && o.hx.perm_hd % 64)
+      return fail(BTF_ERR_ARGS, "step: the perm's tile (perm_hd) must be a multiple of 64");
   } else if (o.hx.block < 0) {
     return fail(BTF_ERR_ARGS, "step: hadamard block must be 0 or a power of two <= 1024");
   }
@@ -1501,17 +1564,23 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   auto q8_of = [&](int v, int k) { return versions[v][k].q8_slot >= 0 ? q8buf[versions[v][k].q8_slot][v] : nullptr; };
   auto f32_of = [&](int v, int k) { return versions[v][k].f32_slot >= 0 ? f32buf[versions[v][k].f32_slot][v] : nullptr; };
   std::vector<PrepDev> preps;
-  auto add_prep = [&](const float* normw, float eps, const btf_hx& hx) {
+  std::vector<std::vector<int>> run_tables;  // uploaded after the program is built
+  std::vector<int> run_of;                   // the prep each table belongs to
+  auto add_prep = [&](const float* normw, float eps, const btf_hx& hx, int n) {
     PrepDev p{};
     p.normw = normw;
     p.eps = eps;
     p.block = hx.block > 0 ? hx.block : 0;
     p.hs = hx.block > 0 ? 1.0f / std::sqrt((float)hx.block) : 1.0f;
     p.signs = hx.block > 0 ? hx.signs : nullptr;
-    if (hx.block > 0 && hx.perm_rep > 1) {
-      p.hd = hx.perm_hd;
-      p.nk = hx.perm_nk;
-      p.rep = hx.perm_rep;
+    if (hx.block > 0 && hx.perm_rep > 1) {  // the gather's runs (perm_hd % 64 == 0: runs of 64 are contiguous)
+      std::vector<int> runs((size_t)n / 64);
+      for (size_t j = 0; j < runs.size(); ++j) {
+        const int og = (int)j * 64, dd = og % hx.perm_hd, t = og / hx.perm_hd;
+        runs[j] = dd + hx.perm_hd * (t / hx.perm_rep + hx.perm_nk * (t % hx.perm_rep));
+      }
+      run_tables.push_back(std::move(runs));
+      run_of.push_back((int)preps.size());
     }
     preps.push_back(p);
     return (int)preps.size() - 1;
@@ -1592,7 +1661,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.codes = u.table_codes;
     o.scales = u.table_scales;
     o.src = u.d_tok;
-    o.prep = add_prep(nullptr, 0.0f, u.hx);
+    o.prep = add_prep(nullptr, 0.0f, u.hx, o.N);
     o.out_plain = final_writer[v] == i ? vecs[v].data : nullptr;
     o.out_q8 = q8_of(v, out_ver[i]);
     o.out_f32 = f32_of(v, out_ver[i]);
@@ -1627,7 +1696,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.up_codes = g.up_codes;
     o.up_scales = g.up_scales;
     const bool pre = has_prep(u);
-    o.prep = pre ? add_prep(u.normw, u.eps, u.hx) : -1;
+    o.prep = pre ? add_prep(u.normw, u.eps, u.hx, g.K) : -1;
     o.in_ll = pre ? f32_of(g.in_vec, in_ver[i]) : q8_of(g.in_vec, in_ver[i]);
     o.in_tag = (uint32_t)dev_writer(g.in_vec, in_ver[i]) + 1;
     o.argmax = i == pick_gemv;
@@ -1757,6 +1826,12 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     head.pos = pick->d_pos;
     if (!(head.parts = static_cast<uint64_t*>(alloc((size_t)G * 2 * 8))))
       return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
+  }
+  for (size_t t = 0; t < run_tables.size(); ++t) {
+    int* d = static_cast<int*>(alloc(run_tables[t].size() * sizeof(int)));
+    if (!d || hipMemcpy(d, run_tables[t].data(), run_tables[t].size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+      return bail(BTF_ERR_LAUNCH, "step: gather table upload failed");
+    preps[run_of[t]].runs = d;
   }
   if (preps.empty()) preps.push_back(PrepDev{});
   P->nops = (int)ops.size();

@@ -127,7 +127,7 @@ class Chain:
             ops += [
                 hip.StepGemv(G.kStore, E, NQ, *d["qkv"], 0, 1, normw=d["attn_norm"], eps=1e-6,
                              hx=hip.Hx(block=256, signs=d["qkv_signs"])),
-                hip.StepGemv(G.kAdd, E, E, *d["o"], 2, 0, hx=hip.Hx(1024, 32, E // 64, 2, d["o_signs"])),
+                hip.StepGemv(G.kAdd, E, E, *d["o"], 2, 0, hx=hip.Hx(1024, 64, E // 128, 2, d["o_signs"])),
                 hip.StepGemv(G.kSwiglu, E, F, *d["gate"], 0, 3, *d["up"], normw=d["ffn_norm"], eps=1e-6,
                              hx=hip.Hx(block=1024)),
                 hip.StepGemv(G.kAdd, F, E, *d["down"], 3, 0, hx=hip.Hx(block=512, signs=d["down_signs"])),
@@ -216,7 +216,7 @@ def test_whole_token_one_layer_pieces_vs_oracle(hip, oracle):
     h = C.host
     specs = [  # (normw, block, perm (hd, nk, rep), signs, matrix, K, mode)
         (L0["attn_norm"], 256, (0, 0, 0), L0["qkv_signs"], L0["qkv"], E, "store"),
-        (None, 1024, (32, E // 64, 2), L0["o_signs"], L0["o"], E, "add"),
+        (None, 1024, (64, E // 128, 2), L0["o_signs"], L0["o"], E, "add"),
         (L0["ffn_norm"], 1024, (0, 0, 0), None, (L0["gate"], L0["up"]), E, "swiglu"),
         (None, 512, (0, 0, 0), L0["down_signs"], L0["down"], F, "add"),
         (h["out_norm"], 1024, (0, 0, 0), h["out_signs"], C.out, E, "store"),
