@@ -9,8 +9,8 @@
 // 76-88: len = 1, 2, 4, ...; x[j] = a + b, x[j + len] = a - b), so it is
 // bit-exact: stages len = 1..8 pair values inside a lane, stages len = 16 ..
 // 512 pair lane l with lane l ^ (len / 16), exchanged by DPP within a row
-// (xor 1, 2 directly; xor 4 and 8 as two mirrors each) and by
-// v_permlane16_swap / v_permlane32_swap across rows.
+// (xor 1, 2 and 8 directly; xor 4 as two moves) and by v_permlane16_swap /
+// v_permlane32_swap across rows.
 #pragma once
 #include "common.h"
 
@@ -20,14 +20,14 @@ constexpr int kSliceVals = 1024;  // values per wave
 
 // Value of lane l ^ X within the 16-lane DPP row (X = 1, 2, 4, 8). A
 // composition dpp<B>(dpp<A>(v)) reads lane srcA(srcB(l)): row_half_mirror is
-// l ^ 7, row_mirror l ^ 15, quad_perm(3,2,1,0) l ^ 3.
+// l ^ 7, quad_perm(3,2,1,0) l ^ 3; a rotation of the row by 8 is l ^ 8.
 template <int X>
 __device__ __forceinline__ float lane_xor(float v) {
   static_assert(X == 1 || X == 2 || X == 4 || X == 8, "DPP exchange within a row");
   if constexpr (X == 1) return dpp_f<0xB1>(v);                // quad_perm(1,0,3,2)
   if constexpr (X == 2) return dpp_f<0x4E>(v);                // quad_perm(2,3,0,1)
   if constexpr (X == 4) return dpp_f<0x1B>(dpp_f<0x141>(v));  // (l ^ 3) ^ 7
-  return dpp_f<0x141>(dpp_f<0x140>(v));                       // (l ^ 7) ^ 15
+  return dpp_f<0x128>(v);                                     // row_ror:8 = l ^ 8
 }
 template <int X>
 __device__ __forceinline__ int lane_xor_i(int v) {
@@ -54,26 +54,41 @@ __device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
 }
 
 // One cross-lane butterfly stage: the lower lane of each pair keeps a + b,
-// the upper a - b (a = the lower lane's value, b the upper's). Without a
-// lane select: each lane adds its partner's value to its own with the sign
-// bit flipped in the upper lane, p + (-v) == p - v exactly in IEEE (so no
-// lane mask is held in scalar registers through the kernel).
+// the upper a - b (a = the lower lane's value, b the upper's).
+//  * X <= 8 (DPP): without a lane select, each lane adds its partner's value
+//    to its own with the sign bit flipped in the upper lane, p + (-v) ==
+//    p - v exactly in IEEE (so no lane mask is held in scalar registers).
+//  * X = 16, 32: two entries at a time through the swaps of two different
+//    registers. v_permlane16_swap(a, b) leaves rows (a0 b0 a2 b2) and
+//    (a1 b1 a3 b3) (row = 16 lanes); v_permlane32_swap(a, b) halves (a_lo
+//    b_lo) and (a_hi b_hi). Their sum and difference hold a + b and a - b of
+//    every pair of both entries, and swapping those two back puts each
+//    entry's sums in its lower lanes and differences in its upper lanes: two
+//    swaps, an add and a subtract per two entries.
 template <int X>
 __device__ __forceinline__ void xstage(float (&v)[16], int lane) {
-  constexpr int kBit = X == 1 ? 0 : X == 2 ? 1 : X == 4 ? 2 : X == 8 ? 3 : X == 16 ? 4 : 5;
-  const uint32_t flip = ((uint32_t)lane >> kBit & 1u) << 31;  // the upper lane negates its own value
+  if constexpr (X <= 8) {
+    constexpr int kBit = X == 1 ? 0 : X == 2 ? 1 : X == 4 ? 2 : 3;
+    const uint32_t flip = ((uint32_t)lane >> kBit & 1u) << 31;  // the upper lane negates its own value
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    if constexpr (X <= 8) {
+    for (int i = 0; i < 16; ++i) {
       const float p = lane_xor<X>(v[i]);
       v[i] = p + __uint_as_float(__float_as_uint(v[i]) ^ flip);
-    } else {
-      float lo, hi;
-      if constexpr (X == 16)
-        pair16(v[i], lo, hi);
-      else
-        pair32(v[i], lo, hi);
-      v[i] = lo + __uint_as_float(__float_as_uint(hi) ^ flip);
+    }
+  } else {
+    static_assert(X == 16 || X == 32, "cross-row stages");
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const auto r = X == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 1]),
+                                                                false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 1]),
+                                                                false, false);
+      const float lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
+      const float sum = lo + hi, dif = lo - hi;
+      const auto t = X == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(sum), __float_as_uint(dif), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(dif), false, false);
+      v[i] = __uint_as_float(t[0]);
+      v[i + 1] = __uint_as_float(t[1]);
     }
   }
 }
@@ -156,6 +171,37 @@ __device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t (&qw)[4],
   }
   s = sum + lane_xor_i<1>(sum);
   d = dd;
+}
+
+// Q8_0 of the 32-value block held by an aligned group of 8 lanes, 4
+// consecutive values per lane (lane l: values 4 (l & 7) .. 4 (l & 7) + 3 of
+// the block): this lane's q word (word l & 7 of the block) and the block's s
+// in every lane of the group, d in its first lane (the one that stores it:
+// the all-zero case reads the sign of value 31, lane 7's v[3], through the
+// half-row mirror). Arithmetic of q8_pair.
+__device__ __forceinline__ uint32_t q8_oct(const float (&v)[4], float& d, int& s) {
+  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  amax = fmaxf(amax, lane_xor<1>(amax));
+  amax = fmaxf(amax, lane_xor<2>(amax));
+  amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the 8
+  const float last = dpp_f<0x141>(v[3]);   // lane 0 of the group <- lane 7
+  float dd = h2f(f2h_bits(amax / 127.0f));
+  if (amax == 0.f) dd = copysignf(0.f, last);
+  const float id = amax != 0.f ? 127.0f / amax : 0.f;
+  int sum = 0;
+  uint32_t w = 0;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int q = (int)__builtin_rintf(v[b] * id);
+    sum += q;
+    w |= (uint32_t)(q & 0xff) << (8 * b);
+  }
+  sum += lane_xor_i<1>(sum);
+  sum += lane_xor_i<2>(sum);
+  sum += dpp_i<0x141>(sum);
+  s = sum;
+  d = dd;
+  return w;
 }
 
 // Canonical sum of squares of a 32-value block, in double: the pairwise tree

@@ -66,7 +66,7 @@ constexpr int kThreads = 64 * (kCW + kIW);  // 768
 constexpr int kRing = 8;                    // weight items (16 B per lane) in flight per compute wave
 constexpr int kMaxK = 20480;                // widest GEMV input
 constexpr int kMaxPart = 8192;              // partial sums per op per workgroup
-constexpr int kMaxOps = 384;                // ops per program (descriptors live in LDS)
+constexpr int kMaxOps = 320;                // ops per program (descriptors live in LDS)
 constexpr int kMaxOld = 1024;               // rows per workgroup of an add-mode op (the LDS carry)
 constexpr int kMaxUnits = 256;              // units of one op per workgroup (kMaxPart / 32)
 constexpr int kWordsPerBlock = 10;          // LL words per 32-value Q8 block
@@ -94,7 +94,8 @@ struct OpDev {
   uint8_t count_reads;  // 1: count the workgroups that have fetched this op's input
   uint8_t out_sq;       // 1: also publish each 32-value block's sum of squares (a later op normalizes it)
   uint8_t argmax;       // 1: the program's greedy pick reads this op's output
-  uint8_t pad0, pad1;
+  uint8_t prep_flags;   // with a prep: bit 0 RMSNorm, bit 1 the tiled -> grouped gather
+  uint8_t pad1;
   const uint8_t* codes;     // GEMV: weights (swiglu: gate); embedding: table codes
   const uint16_t* scales;   // embedding: table scales
   const uint8_t* up_codes;
@@ -179,6 +180,7 @@ struct Lds {
   uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
   uint64_t argk[kIW];         // per I/O wave: the largest pick key of the rows it published
   uint32_t sready[2][kMaxK / kSliceVals];  // prep inputs: op index + 1 once slice sl of buffer ob is in LDS
+  float stg[kCW][256];        // per compute wave: the prep's Q8 transposition
   WorkRec wrec[kRecSlots][kCW];
   OpRec orec[kRecSlots];
   const PrepDev* preps;  // kernel arguments read where needed (not held in
@@ -200,6 +202,25 @@ __device__ __forceinline__ bool grid_failed(const Ctl* ctl, const Lds& L) {
 __device__ __forceinline__ void set_abort(Lds& L, Ctl* ctl) {
   __hip_atomic_store(&ctl->error, L.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(&L.abort_, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Address-space views of pointers. A pointer staged in LDS comes back
+// generic, and a load through a generic pointer is a flat instruction, which
+// counts in both vmcnt and lgkmcnt: a wait for its result waits for every
+// global load issued before it (the weight stream in flight). Descriptors are
+// read through the constant space (scalar loads), data through the global
+// space.
+template <class T>
+using cptr = const __attribute__((address_space(4))) T*;
+template <class T>
+using gptr = const __attribute__((address_space(1))) T*;
+template <class T>
+__device__ __forceinline__ cptr<T> as_const(const T* p) {
+  return (cptr<T>)p;
+}
+template <class T>
+__device__ __forceinline__ gptr<T> as_global(const T* p) {
+  return (gptr<T>)p;
 }
 
 __device__ __forceinline__ int sgpr(int v) { return __builtin_amdgcn_readfirstlane(v); }
@@ -344,7 +365,7 @@ struct PrepRegs {  // a PrepDev in scalar registers
   bool perm;
 };
 __device__ __forceinline__ PrepRegs prep_regs(const PrepDev* preps, int i) {
-  const PrepDev& p = preps[i];
+  const auto& p = as_const(preps)[i];
   PrepRegs r;
   r.normw = sgpr_ptr(p.normw);
   r.signs = sgpr_ptr(p.signs);
@@ -399,37 +420,58 @@ __device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd,
 // Slice sl of a prep GEMV's input into LDS buffer `ob` (Q8 image). The wave
 // holds the slice strided (slice.h): lane l takes values sl * 1024 + l + 64 i,
 // so every LL load instruction reads 64 consecutive words (512 contiguous
-// bytes); the 32-value Q8 block of entry i is then the half-wave
-// (lane >> 5) at i (the producers' q8_half), and four consecutive lanes
-// pack their q bytes into one word. With the perm, each 64-value run comes
+// bytes). The slice's loads, and those of its norm weights and signs, are
+// all issued before the first wait: with `scale_due`, the wait for the
+// RMSNorm scale (every producer of the vector) runs while they are in
+// flight. After the transform, the Q8 runs in four rounds of 256 values:
+// the round's four entries are transposed through the wave's 1 KB of LDS
+// staging, so that lane l holds values 4 l .. 4 l + 3 of the round and each
+// 32-value block is an aligned group of 8 lanes (q8_oct: one reduction per
+// round instead of one per entry). With the perm, each 64-value run comes
 // from 64 consecutive sources (the step program takes perm_hd % 64 == 0), so
 // the gather costs one uniform source index per run, recomputed at each use
 // (an empty asm keeps the compiler from holding 16 of them in registers).
 template <bool PERM>
-__device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev* preps, int pi, float scale, Lds& L,
-                                                 int lane, Ctl* ctl, uint32_t base_tag, int ob, int sl) {
+__device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev* preps, int pi, float& scale,
+                                                 bool scale_due, Lds& L, int wave, int lane, Ctl* ctl,
+                                                 uint32_t base_tag, int ob, int sl) {
   // Each field of the prep is loaded (a scalar load) where it is used: the
   // pointer passes an empty asm before every use, so no field is held in
   // scalar registers across the polls.
   auto P = [&]() {
-    const PrepDev* p = preps + pi;
+    cptr<PrepDev> p = as_const(preps) + pi;
     asm volatile("" : "+s"(p));
     return p;
   };
   const uint64_t* in = sgpr_ptr(op.in_ll);
-  const uint32_t tin = base_tag + sgpr(op.in_tag);
   const int c = sl * kSliceVals;
   // word index of entry i of this lane: with the perm, run i's first source
   // from the program's table (a scalar load at each use), plus the lane
   auto src = [&](int i) {
     if constexpr (PERM)
-      return P()->runs[(c >> 6) + i] + lane;  // (no readfirstlane: the reload below is under a lane mask)
+      return as_const(P()->runs)[(c >> 6) + i] + lane;  // (no readfirstlane: the reload below is under a lane mask)
     else
       return c + 64 * i + lane;
   };
   uint64_t w[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) w[i] = ll_load(in + src(i));
+  // one factor per entry loaded before the waits: the norm weight, or
+  // without a norm the sign (with both, the signs are loaded after the wait:
+  // registers are short)
+  float pre[16];
+  const PrepRegs pd = prep_regs(preps, pi);  // the descriptor in one burst of scalar loads
+  const gptr<float> normw = as_global(pd.normw);
+  const gptr<float> signs = as_global(pd.block > 0 ? pd.signs : nullptr);
+  if (normw) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pre[i] = normw[src(i)];
+  } else if (signs) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) pre[i] = signs[c + 64 * i + lane];
+  }
+  if (scale_due) scale = prep_scale(op, pd, L, lane, ctl, base_tag);
+  const uint32_t tin = base_tag + sgpr(op.in_tag);
   uint32_t spins = 0;
   for (;;) {
     uint32_t pending = 0;
@@ -446,33 +488,45 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev*
   float v[16];
 #pragma unroll
   for (int i = 0; i < 16; ++i) v[i] = __uint_as_float((uint32_t)w[i]);
-  if (const float* normw = sgpr_ptr(P()->normw))
+  if (normw) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * normw[src(i)];
-  if (const int block = sgpr(P()->block); block > 0) {
-    if (const float* signs = sgpr_ptr(P()->signs))
+    for (int i = 0; i < 16; ++i) v[i] = (v[i] * scale) * pre[i];
+    if (signs)
 #pragma unroll
       for (int i = 0; i < 16; ++i) v[i] = v[i] * signs[c + 64 * i + lane];
-    slice_fwht_strided(v, lane, block);
-    const float hs = __int_as_float(sgpr(__float_as_int(P()->hs)));
+  } else if (signs) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) v[i] = v[i] * hs;
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * pre[i];
+  }
+  if (pd.block > 0) {
+    slice_fwht_strided(v, lane, pd.block);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) v[i] = v[i] * pd.hs;
   }
   int lq = lane;
   asm volatile("" : "+v"(lq));  // lane tests formed here, not held from the kernel's start
-  const int j = lq & 31, h = lq >> 5;
+  const int j = lq & 7, g = lq >> 3;
+  float* stg = L.stg[wave];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int r = 0; r < 4; ++r) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) stg[64 * k + lq] = v[4 * r + k];
+    // (a wave's LDS operations complete in order: the reads below see every
+    // lane's writes, and the next round's writes follow these reads)
+    asm volatile("" ::: "memory");
+    typedef float f32x4 __attribute__((ext_vector_type(4)));
+    const f32x4 x4 = *reinterpret_cast<const f32x4*>(stg + 4 * lq);
+    const float x[4] = {x4[0], x4[1], x4[2], x4[3]};
     float d;
     int s;
-    const int q = q8_half(v[i], d, s);
-    const uint32_t b = (uint32_t)(q & 0xff) << (8 * (j & 3));
-    uint32_t wq = b | (uint32_t)dpp_i<0xB1>((int)b);  // quad_perm(1,0,3,2)
-    wq |= (uint32_t)dpp_i<0x4E>((int)wq);             // quad_perm(2,3,0,1)
-    uint32_t* dst = &L.act[ob][(sl * 32 + 2 * i + h) * kWordsPerBlock];
-    if ((j & 3) == 0) dst[j >> 2] = wq;
-    if (j == 0) dst[8] = __float_as_uint(d);
-    if (j == 1) dst[9] = (uint32_t)s;
+    const uint32_t wq = q8_oct(x, d, s);
+    uint32_t* dst = &L.act[ob][(sl * 32 + 8 * r + g) * kWordsPerBlock];
+    dst[j] = wq;
+    if (j == 0) {
+      dst[8] = __float_as_uint(d);
+      dst[9] = (uint32_t)s;
+    }
+    asm volatile("" ::: "memory");
   }
 }
 
@@ -840,16 +894,12 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     const int pi = sgpr(L.opd[opi].prep);
     if (pi >= 0 && wave < sgpr(L.opd[opi].K) / kSliceVals) {
       float scale = 1.0f;
-      bool perm;
-      {
-        const PrepRegs pd = prep_regs(sgpr_ptr(L.preps), pi);
-        perm = pd.perm;
-        if (pd.normw) scale = prep_scale(L.opd[opi], pd, L, lane, ctl, base_tag);
-      }
+      const int pf = sgpr(L.opd[opi].prep_flags);
+      const bool norm = (pf & 1) != 0, perm = (pf & 2) != 0;
       auto mine = [&](auto pm) {
         for (int sl = wave; sl < sgpr(L.opd[opi].K) / kSliceVals; sl += kCW) {
-          fetch_prep_slice<decltype(pm)::value>(L.opd[opi], sgpr_ptr(L.preps), sgpr(L.opd[opi].prep), scale, L,
-                                                lane, ctl, base_tag, ob, sl);
+          fetch_prep_slice<decltype(pm)::value>(L.opd[opi], sgpr_ptr(L.preps), sgpr(L.opd[opi].prep), scale,
+                                                norm && sl == wave, L, wave, lane, ctl, base_tag, ob, sl);
           asm volatile("" ::: "memory");  // the image words before the flag (LDS ops of a wave complete in order)
           __hip_atomic_store(&L.sready[ob][sl], (uint32_t)opi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
@@ -1058,8 +1108,8 @@ __device__ __forceinline__ void io_embed(const OpDev& op, const PrepRegs& pd, in
   const int iw = iol >> 6, lane = iol & 63;
   const int E = sgpr(op.N), units = sgpr(op.units);
   const int tok = sgpr(*(const __attribute__((address_space(1))) int*)sgpr_ptr(static_cast<const int*>(op.src)));
-  const uint32_t* rowc = reinterpret_cast<const uint32_t*>(sgpr_ptr(op.codes) + (size_t)tok * (size_t)(E / 4));
-  const uint16_t* rows = sgpr_ptr(op.scales) + (size_t)tok * (size_t)(E / 128);
+  const gptr<uint32_t> rowc = as_global(reinterpret_cast<const uint32_t*>(sgpr_ptr(op.codes) + (size_t)tok * (size_t)(E / 4)));
+  const gptr<uint16_t> rows = as_global(sgpr_ptr(op.scales) + (size_t)tok * (size_t)(E / 128));
   for (int u = first_unit(sgpr(op.rot), wg, G) + iw * G; u < units; u += kIW * G) {
     const int c0 = u * kSliceVals + 16 * lane;
     const uint32_t w = rowc[c0 >> 4];
@@ -1071,9 +1121,9 @@ __device__ __forceinline__ void io_embed(const OpDev& op, const PrepRegs& pd, in
       slice_fwht(v, lane, pd.block);
 #pragma unroll
       for (int j = 0; j < 16; ++j) v[j] = v[j] * pd.hs;
-      if (pd.signs)
+      if (const gptr<float> signs = as_global(pd.signs))
 #pragma unroll
-        for (int j = 0; j < 16; ++j) v[j] = v[j] * pd.signs[c0 + j];
+        for (int j = 0; j < 16; ++j) v[j] = v[j] * signs[c0 + j];
     }
     publish_slice(op, c0, lane, v, tag);
   }
@@ -1201,8 +1251,9 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
 // The program's greedy pick (workgroup 0's first I/O wave, after its last
 // op): the largest of the G workgroups' keys, polled from their LL words.
 __device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int lane, Ctl* ctl, uint32_t base_tag) {
-  const uint64_t* parts = sgpr_ptr(head->parts);
-  const uint32_t tag = base_tag + sgpr((int)head->tag);
+  const cptr<HeadDev> h = as_const(head);
+  const uint64_t* parts = sgpr_ptr(h->parts);
+  const uint32_t tag = base_tag + sgpr((int)h->tag);
   constexpr int kPer = 4;  // parts per lane (G <= 256)
   uint64_t lo[kPer], hi[kPer];
 #pragma unroll
@@ -1233,9 +1284,10 @@ __device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int 
     if (lane + 64 * b < G) best = key_max(best, ((uint64_t)(uint32_t)hi[b] << 32) | (uint32_t)lo[b]);
   best = wave_max_key(best);
   if (first_lane(lane)) {
-    *(__attribute__((address_space(1))) int*)sgpr_ptr(head->tok_out) = argmax_key_index(best);
-    int* pos = sgpr_ptr(head->pos);
-    if (pos) (void)__hip_atomic_fetch_add(pos, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *(__attribute__((address_space(1))) int*)sgpr_ptr(h->tok_out) = argmax_key_index(best);
+    if (int* pos = sgpr_ptr(h->pos))
+      (void)__hip_atomic_fetch_add((__attribute__((address_space(1))) int*)pos, 1, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1277,14 +1329,14 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
       const uint64_t k = key_max(L.argk[0], L.argk[1]);
-      uint64_t* dst = sgpr_ptr(sgpr_ptr(L.head)->parts) + 2 * wg;
+      uint64_t* dst = sgpr_ptr(as_const(sgpr_ptr(L.head))->parts) + 2 * wg;
       const uint32_t tag = base_tag + sgpr(op.my_tag);
       ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)k);
       ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(k >> 32));
     }
     if (!early_done) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, true, (uint32_t)nx + 1);
   }
-  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(sgpr_ptr(L.head)->present)) io_pick(sgpr_ptr(L.head), L, G, iol, ctl, base_tag);
+  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(as_const(sgpr_ptr(L.head))->present)) io_pick(sgpr_ptr(L.head), L, G, iol, ctl, base_tag);
 }
 
 // ---------------------------------------------------------------- the kernel
@@ -1585,6 +1637,9 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     preps.push_back(p);
     return (int)preps.size() - 1;
   };
+  auto prep_flags_of = [](const float* normw, const btf_hx& hx) {
+    return (uint8_t)((normw ? 1 : 0) | (hx.block > 0 && hx.perm_rep > 1 ? 2 : 0));
+  };
   // ---- the device program: prologue quantize ops, embeddings, then the GEMVs in order
   std::vector<OpDev> ops;
   // known[v * G + w]: the last GEMV whose barrier B workgroup w has surely
@@ -1662,6 +1717,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.scales = u.table_scales;
     o.src = u.d_tok;
     o.prep = add_prep(nullptr, 0.0f, u.hx, o.N);
+    o.prep_flags = prep_flags_of(nullptr, u.hx);
     o.out_plain = final_writer[v] == i ? vecs[v].data : nullptr;
     o.out_q8 = q8_of(v, out_ver[i]);
     o.out_f32 = f32_of(v, out_ver[i]);
@@ -1697,6 +1753,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.up_scales = g.up_scales;
     const bool pre = has_prep(u);
     o.prep = pre ? add_prep(u.normw, u.eps, u.hx, g.K) : -1;
+    o.prep_flags = pre ? prep_flags_of(u.normw, u.hx) : 0;
     o.in_ll = pre ? f32_of(g.in_vec, in_ver[i]) : q8_of(g.in_vec, in_ver[i]);
     o.in_tag = (uint32_t)dev_writer(g.in_vec, in_ver[i]) + 1;
     o.argmax = i == pick_gemv;
@@ -1783,7 +1840,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     prev_gemv.push_back(last_gemv);
     last_gemv = me;
   }
-  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 384 ops (prologue + GEMVs)");
+  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 320 ops (prologue + GEMVs)");
   // Early fetch and carry. An op's input is fetched by the I/O waves while
   // the previous GEMV computes when every producer it reads from comes
   // before that previous GEMV (a workgroup then never waits for its own
