@@ -66,14 +66,14 @@ constexpr int kThreads = 64 * (kCW + kIW);  // 768
 constexpr int kRing = 8;                    // weight items (16 B per lane) in flight per compute wave
 constexpr int kMaxK = 20480;                // widest GEMV input
 constexpr int kMaxPart = 8192;              // partial sums per op per workgroup
-constexpr int kMaxOps = 320;                // ops per program (descriptors live in LDS)
+constexpr int kMaxOps = 300;                // ops per program (descriptors live in LDS)
 constexpr int kMaxOld = 1024;               // rows per workgroup of an add-mode op (the LDS carry)
 constexpr int kMaxUnits = 256;              // units of one op per workgroup (kMaxPart / 32)
 constexpr int kWordsPerBlock = 10;          // LL words per 32-value Q8 block
 constexpr int kSlots = 3;                   // LL buffers of each kind per vector (versions in turn)
 constexpr uint32_t kSpinMax = 1u << 20;     // poll bound (each poll is a memory round trip: ~1 s)
 
-// 144 bytes (a multiple of 16: copied into LDS in 16-byte words).
+// 176 bytes (a multiple of 16: copied into LDS in 16-byte words).
 struct OpDev {
   int kind;  // 0 = quantize a user vector (prologue), 1 = GEMV, 2 = embedding lookup (prologue)
   int mode;
@@ -107,12 +107,19 @@ struct OpDev {
   uint64_t* out_q8;         // LL Q8 of the output vector (nullable)
   const uint64_t* old_f32;  // add mode: previous value of the output vector
   const void* src;          // quantize: user vector (float); embedding: token id (int)
+  // the prep's fields (copies of its PrepDev, here in LDS with the rest)
+  const float* normw;       // RMSNorm weights (NULL: none)
+  const float* signs;       // transform signs (NULL: none)
+  float eps, hs;            // RMSNorm epsilon; 1 / sqrtf(block)
+  int block;                // transform block (0: none)
+  int pad2;
 };
-static_assert(sizeof(OpDev) == 144, "descriptor layout");
+static_assert(sizeof(OpDev) == 176, "descriptor layout");
 
-// An op's activation prep (global memory, read with scalar loads once per op
-// per wave): launch_prep's pipeline for a GEMV input, or the inverse
-// transform of an embedding lookup (normw = NULL).
+// An op's activation prep: launch_prep's pipeline for a GEMV input, or the
+// inverse transform of an embedding lookup (normw = NULL). The host copies
+// every field but `runs` into the op's descriptor (LDS); the kernel reads
+// only the gather's run table from here (global memory, scalar loads).
 struct PrepDev {
   const float* normw;  // NULL: no RMSNorm
   const float* signs;  // NULL: none
@@ -357,22 +364,19 @@ __device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t 
 // copied the producer's Q8 words. Bit-identical to launch_prep on the same
 // fp32 vector: the same per-slice arithmetic, and the RMSNorm scale from the
 // producers' block sums of squares summed in prep_slices_kernel's order.
-struct PrepRegs {  // a PrepDev in scalar registers
+struct PrepRegs {  // an op's prep fields in scalar registers
   const float* normw;
   const float* signs;
   float eps, hs;
   int block;
-  bool perm;
 };
-__device__ __forceinline__ PrepRegs prep_regs(const PrepDev* preps, int i) {
-  const auto& p = as_const(preps)[i];
+__device__ __forceinline__ PrepRegs prep_regs(const OpDev& op) {  // (from the LDS copy of the op)
   PrepRegs r;
-  r.normw = sgpr_ptr(p.normw);
-  r.signs = sgpr_ptr(p.signs);
-  r.eps = __int_as_float(sgpr(__float_as_int(p.eps)));
-  r.hs = __int_as_float(sgpr(__float_as_int(p.hs)));
-  r.block = sgpr(p.block);
-  r.perm = sgpr_ptr(p.runs) != nullptr;
+  r.normw = sgpr_ptr(op.normw);
+  r.signs = sgpr_ptr(op.signs);
+  r.eps = __int_as_float(sgpr(__float_as_int(op.eps)));
+  r.hs = __int_as_float(sgpr(__float_as_int(op.hs)));
+  r.block = sgpr(op.block);
   return r;
 }
 
@@ -460,7 +464,7 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev*
   // without a norm the sign (with both, the signs are loaded after the wait:
   // registers are short)
   float pre[16];
-  const PrepRegs pd = prep_regs(preps, pi);  // the descriptor in one burst of scalar loads
+  const PrepRegs pd = prep_regs(op);
   const gptr<float> normw = as_global(pd.normw);
   const gptr<float> signs = as_global(pd.block > 0 ? pd.signs : nullptr);
   if (normw) {
@@ -506,17 +510,24 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev*
   int lq = lane;
   asm volatile("" : "+v"(lq));  // lane tests formed here, not held from the kernel's start
   const int j = lq & 7, g = lq >> 3;
+  // The four transpositions back to back (a wave's LDS operations complete
+  // in order: each round's reads see every lane's writes, and the next
+  // round's writes follow those reads; the empty asms keep the compiler's
+  // order), then the four rounds' Q8 with no LDS wait between them.
   float* stg = L.stg[wave];
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  f32x4 x4[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) stg[64 * k + lq] = v[4 * r + k];
-    // (a wave's LDS operations complete in order: the reads below see every
-    // lane's writes, and the next round's writes follow these reads)
     asm volatile("" ::: "memory");
-    typedef float f32x4 __attribute__((ext_vector_type(4)));
-    const f32x4 x4 = *reinterpret_cast<const f32x4*>(stg + 4 * lq);
-    const float x[4] = {x4[0], x4[1], x4[2], x4[3]};
+    x4[r] = *reinterpret_cast<const f32x4*>(stg + 4 * lq);
+    asm volatile("" ::: "memory");
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float x[4] = {x4[r][0], x4[r][1], x4[r][2], x4[r][3]};
     float d;
     int s;
     const uint32_t wq = q8_oct(x, d, s);
@@ -526,7 +537,6 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev*
       dst[8] = __float_as_uint(d);
       dst[9] = (uint32_t)s;
     }
-    asm volatile("" ::: "memory");
   }
 }
 
@@ -1306,7 +1316,7 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       continue;
     }
     if (kind == 2) {
-      io_embed(op, prep_regs(sgpr_ptr(L.preps), sgpr(op.prep)), wg, G, iol, base_tag + sgpr(op.my_tag));
+      io_embed(op, prep_regs(op), wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
     const int nx = sgpr(op.next);
@@ -1640,6 +1650,17 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   auto prep_flags_of = [](const float* normw, const btf_hx& hx) {
     return (uint8_t)((normw ? 1 : 0) | (hx.block > 0 && hx.perm_rep > 1 ? 2 : 0));
   };
+  auto set_prep = [&](OpDev& o, int pi, const btf_hx& hx) {  // the op's copy of the prep's fields
+    o.prep = pi;
+    if (pi < 0) return;
+    const PrepDev& p = preps[(size_t)pi];
+    o.normw = p.normw;
+    o.signs = p.signs;
+    o.eps = p.eps;
+    o.hs = p.hs;
+    o.block = p.block;
+    o.prep_flags = prep_flags_of(p.normw, hx);
+  };
   // ---- the device program: prologue quantize ops, embeddings, then the GEMVs in order
   std::vector<OpDev> ops;
   // known[v * G + w]: the last GEMV whose barrier B workgroup w has surely
@@ -1716,8 +1737,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.codes = u.table_codes;
     o.scales = u.table_scales;
     o.src = u.d_tok;
-    o.prep = add_prep(nullptr, 0.0f, u.hx, o.N);
-    o.prep_flags = prep_flags_of(nullptr, u.hx);
+    set_prep(o, add_prep(nullptr, 0.0f, u.hx, o.N), u.hx);
     o.out_plain = final_writer[v] == i ? vecs[v].data : nullptr;
     o.out_q8 = q8_of(v, out_ver[i]);
     o.out_f32 = f32_of(v, out_ver[i]);
@@ -1752,8 +1772,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     o.up_codes = g.up_codes;
     o.up_scales = g.up_scales;
     const bool pre = has_prep(u);
-    o.prep = pre ? add_prep(u.normw, u.eps, u.hx, g.K) : -1;
-    o.prep_flags = pre ? prep_flags_of(u.normw, u.hx) : 0;
+    set_prep(o, pre ? add_prep(u.normw, u.eps, u.hx, g.K) : -1, u.hx);
     o.in_ll = pre ? f32_of(g.in_vec, in_ver[i]) : q8_of(g.in_vec, in_ver[i]);
     o.in_tag = (uint32_t)dev_writer(g.in_vec, in_ver[i]) + 1;
     o.argmax = i == pick_gemv;
@@ -1840,7 +1859,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     prev_gemv.push_back(last_gemv);
     last_gemv = me;
   }
-  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 320 ops (prologue + GEMVs)");
+  if ((int)ops.size() > kMaxOps) return bail(BTF_ERR_ARGS, "step: more than 300 ops (prologue + GEMVs)");
   // Early fetch and carry. An op's input is fetched by the I/O waves while
   // the previous GEMV computes when every producer it reads from comes
   // before that previous GEMV (a workgroup then never waits for its own
