@@ -482,7 +482,7 @@ def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full"):
         "verified": "step program bit-exact vs the op-by-op launches (vectors, token, position)",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "step_kernel (the whole token, one launch)", "bytes_per_launch": T.total_bytes,
+                     "kernel": "step_kernel<true> (the whole token, one launch)", "bytes_per_launch": T.total_bytes,
                      "avg_launch_us": round(ms * 1e3, 3)},
     }
 
@@ -1083,7 +1083,7 @@ def main():
         roof = {"bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(value / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
                 "traffic_source": tr["source"] if tr else None,
-                "kernel": "step_kernel (the whole GEMV chain, one launch per step)",
+                "kernel": "step_kernel<false> (the whole GEMV chain, one launch per step)",
                 "bytes_per_launch": step.total_bytes, "avg_launch_us": round(ms * 1e3, 3)}
     elif step.M == 1:
         dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])

@@ -875,6 +875,7 @@ __device__ __forceinline__ bool sum_lanes(int l16) {
 // compiler keeps each slot in fixed registers with exact wait counts; the
 // per-batch bookkeeping (addresses, partial-sum slots, the unit's count, the
 // activation reload at a new slice) is uniform and done once per batch.
+template <bool kFull>
 __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
                                               uint32_t base_tag) {
   const int l16 = lane & 15, grp = lane >> 4;
@@ -901,7 +902,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
     // per workgroup into the LDS image and flagged -- by every wave with a
     // share, whether or not it has items of the op; below, every wave with
     // items waits for the flags of the slices its items read.
-    const int pi = sgpr(L.opd[opi].prep);
+    const int pi = kFull ? sgpr(L.opd[opi].prep) : -1;
     if (pi >= 0 && wave < sgpr(L.opd[opi].K) / kSliceVals) {
       float scale = 1.0f;
       const int pf = sgpr(L.opd[opi].prep_flags);
@@ -1306,6 +1307,7 @@ __device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int 
 // units as they complete, barrier B, count this workgroup's reads of the
 // op's input (and publish its pick key), finish the early fetch. Prologue ops
 // (quantize, embedding) run before the first GEMV.
+template <bool kFull>
 __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
                                          uint32_t base_tag) {
   for (int i = 0; i < nops; ++i) {
@@ -1315,7 +1317,7 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
       io_quantize(op, wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
-    if (kind == 2) {
+    if (kFull && kind == 2) {
       io_embed(op, prep_regs(op), wg, G, iol, base_tag + sgpr(op.my_tag));
       continue;
     }
@@ -1337,7 +1339,7 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     const bool io0 = sgpr(iol >> 6) == 0;  // the first I/O wave
     if (sgpr(op.count_reads) && io0 && first_lane(iol))
       (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
+    if (kFull && sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
       const uint64_t k = key_max(L.argk[0], L.argk[1]);
       uint64_t* dst = sgpr_ptr(as_const(sgpr_ptr(L.head))->parts) + 2 * wg;
       const uint32_t tag = base_tag + sgpr(op.my_tag);
@@ -1346,10 +1348,15 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     }
     if (!early_done) early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, true, (uint32_t)nx + 1);
   }
-  if (wg == 0 && sgpr(iol >> 6) == 0 && sgpr(as_const(sgpr_ptr(L.head))->present)) io_pick(sgpr_ptr(L.head), L, G, iol, ctl, base_tag);
+  if (kFull && wg == 0 && sgpr(iol >> 6) == 0 && sgpr(as_const(sgpr_ptr(L.head))->present))
+    io_pick(sgpr_ptr(L.head), L, G, iol, ctl, base_tag);
 }
 
 // ---------------------------------------------------------------- the kernel
+// Two instances: kFull for programs with an activation prep, an embedding
+// lookup or a greedy pick; the plain one (a chain of GEMVs on Q8 inputs)
+// without that code.
+template <bool kFull>
 __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict__ ops, int nops, int first_gemv,
                                                         Ctl* ctl, uint32_t* rd_cnt, const PrepDev* __restrict__ preps,
                                                         const HeadDev* __restrict__ head) {
@@ -1385,13 +1392,13 @@ __global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict_
   const uint32_t base_tag = L.epoch * (uint32_t)(nops + 1);
 
   if (wave < kCW)
-    compute_waves(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
+    compute_waves<kFull>(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
   else {
     // The I/O waves' epilogue of an op is on the chain's critical path while
     // the compute waves already run the next op's dot products on the same
     // SIMDs: their instructions issue first (the waits in between sleep).
     __builtin_amdgcn_s_setprio(3);
-    io_waves(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
+    io_waves<kFull>(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
     __builtin_amdgcn_s_setprio(0);
   }
 
@@ -1425,6 +1432,7 @@ struct StepProgram {
   uint32_t* d_cnt = nullptr;    // per-op reader counters
   PrepDev* d_preps = nullptr;   // the ops' prep descriptors
   HeadDev* d_head = nullptr;    // the greedy pick
+  bool full = false;            // any prep, embedding or pick: the kFull kernel
   std::vector<void*> bufs;      // every device buffer the program owns
 };
 
@@ -1909,6 +1917,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
       return bail(BTF_ERR_LAUNCH, "step: gather table upload failed");
     preps[run_of[t]].runs = d;
   }
+  P->full = pick != nullptr || std::any_of(ops.begin(), ops.end(), [](const OpDev& o) { return o.prep >= 0 || o.kind == 2; });
   if (preps.empty()) preps.push_back(PrepDev{});
   P->nops = (int)ops.size();
   if (!(P->d_ops = static_cast<OpDev*>(alloc(ops.size() * sizeof(OpDev)))) ||
@@ -1947,9 +1956,11 @@ int step_check_residency(const DevState& ds) {
     return fail(BTF_ERR_DEVICE, "step: device query failed");
   if (!coop) return fail(BTF_ERR_DEVICE, "step: the device does not support cooperative launches");
   int per_cu = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel, kThreads, 0) != hipSuccess)
-    return fail(BTF_ERR_LAUNCH, "step: occupancy query failed");
-  if (per_cu < 1) return fail(BTF_ERR_LAUNCH, "step: the step kernel does not fit on a CU");
+  for (const void* k : {reinterpret_cast<const void*>(step_kernel<false>), reinterpret_cast<const void*>(step_kernel<true>)}) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess)
+      return fail(BTF_ERR_LAUNCH, "step: occupancy query failed");
+    if (per_cu < 1) return fail(BTF_ERR_LAUNCH, "step: the step kernel does not fit on a CU");
+  }
   (void)ds;
   return BTF_OK;
 }
@@ -1960,7 +1971,9 @@ int step_launch(StepProgram* P, hipStream_t st) {
     return fail(BTF_ERR_ARGS, "step: launch on a device other than the program's");
   void* args[] = {&P->d_ops, &P->nops, &P->first, &P->d_ctl, &P->d_cnt, &P->d_preps, &P->d_head};
   const hipError_t e =
-      hipLaunchCooperativeKernel(reinterpret_cast<const void*>(step_kernel), dim3(P->G), dim3(kThreads), args, 0, st);
+      hipLaunchCooperativeKernel(P->full ? reinterpret_cast<const void*>(step_kernel<true>)
+                                         : reinterpret_cast<const void*>(step_kernel<false>),
+                                 dim3(P->G), dim3(kThreads), args, 0, st);
   if (e != hipSuccess) return fail(BTF_ERR_LAUNCH, std::string("step kernel: ") + hipGetErrorString(e));
   return launch_status("step_kernel");
 }
