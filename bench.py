@@ -437,7 +437,7 @@ class Token:
         hip.launch_pos_add(self.pos, 1, st)
 
 
-def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full"):
+def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full", traffic_tab=None):
     """The whole decode step: one step-program launch per token, checked
     bit-exact against the op-by-op launches (vectors, token, position), then
     both timed over `steps` tokens (each decoding the previous pick)."""
@@ -469,6 +469,7 @@ def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full"):
     T.reset()
     gms = time_graph(hip, torch, T.run, steps, warmup)
     gbs = T.total_bytes / (ms * 1e-3) / 1e9
+    tr = (traffic_tab or {}).get("token/step_kernel") if prep == "full" and layers == LAYERS else None
     log(f"whole token: step program {ms:.4f} ms ({1e3 / ms:.1f} tok/s, {gbs:.1f} GB/s), "
         f"op-by-op graph {gms:.4f} ms ({1e3 / gms:.1f} tok/s)")
     return {
@@ -481,7 +482,8 @@ def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full"):
         "kernels_per_token": {"step": 1, "graph": 2 + 2 * (4 * layers + 1) + 2},
         "verified": "step program bit-exact vs the op-by-op launches (vectors, token, position)",
         "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
+                     "traffic_source": tr["source"] if tr else None,
                      "kernel": "step_kernel<true> (the whole token, one launch)", "bytes_per_launch": T.total_bytes,
                      "avg_launch_us": round(ms * 1e3, 3)},
     }
@@ -948,7 +950,7 @@ def main():
         traffic_tab = {}
 
     if args.workload == "token":
-        tok = run_token(S, hip, torch, layers, args.steps, args.warmup, args.token_prep)
+        tok = run_token(S, hip, torch, layers, args.steps, args.warmup, args.token_prep, traffic_tab)
         out = {"metric": "whole-token decode step at batch 1 (tok/s)", "value": tok["tok_s"], "unit": "tok/s",
                "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": tok["ms_per_token"],
                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
@@ -1103,7 +1105,7 @@ def main():
     # (batched decode M = 8) and config 4 (prefill M = 512) on 8 layers.
     subs = None
     if subs_on:
-        subs = {"whole_token": run_token(S, hip, torch, layers, args.steps, args.warmup)}
+        subs = {"whole_token": run_token(S, hip, torch, layers, args.steps, args.warmup, traffic_tab=traffic_tab)}
         if "o" in per:
             d = per["o"]
             subs["config1_gemv_5120x5120"] = {
