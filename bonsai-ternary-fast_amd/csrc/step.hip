@@ -60,9 +60,22 @@ namespace {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int kCW = 10;                     // compute waves
-constexpr int kIW = 2;                      // I/O waves
-constexpr int kThreads = 64 * (kCW + kIW);  // 768
+// Compute waves per workgroup, per kernel instance: three waves per SIMD
+// (the full kernel needs 164 VGPRs). The plain instance also fits 14 compute
+// waves at 128 VGPRs (four per SIMD, 40 % more weight bytes in flight), but
+// the step then takes 5 % longer: the I/O waves, which publish each op's
+// units on the chain's critical path, share their SIMDs with three compute
+// waves instead of two.
+constexpr int kCWFull = 10, kCWPlain = 10;
+constexpr int kIW = 2;  // I/O waves
+template <bool kFull>
+constexpr int cw_of() {
+  return kFull ? kCWFull : kCWPlain;
+}
+template <bool kFull>
+constexpr int threads_of() {
+  return 64 * (cw_of<kFull>() + kIW);
+}
 constexpr int kRing = 8;                    // weight items (16 B per lane) in flight per compute wave
 constexpr int kMaxK = 20480;                // widest GEMV input
 constexpr int kMaxPart = 8192;              // partial sums per op per workgroup
@@ -176,7 +189,9 @@ struct OpRec {
 };
 constexpr int kRecSlots = 3;  // records of ops i, i + 1, i + 2 (slot = op index % 3)
 
+template <bool kFull>
 struct Lds {
+  static constexpr int kCW = cw_of<kFull>();
   OpDev opd[kMaxOps];        // the program
   // An op's Q8 input (by op parity) as the image of its LL words: per
   // 32-value block 8 words of q bytes, d (f32 bits), s.
@@ -187,7 +202,7 @@ struct Lds {
   uint32_t early_seq[kIW];    // per I/O wave: op index + 1 of the last input it fetched early
   uint64_t argk[kIW];         // per I/O wave: the largest pick key of the rows it published
   uint32_t sready[2][kMaxK / kSliceVals];  // prep inputs: op index + 1 once slice sl of buffer ob is in LDS
-  float stg[kCW][256];        // per compute wave: the prep's Q8 transposition
+  float stg[kFull ? kCW : 1][256];  // per compute wave: the prep's Q8 transposition
   WorkRec wrec[kRecSlots][kCW];
   OpRec orec[kRecSlots];
   const PrepDev* preps;  // kernel arguments read where needed (not held in
@@ -197,16 +212,19 @@ struct Lds {
   uint32_t spin_max;
 };
 
-__device__ __forceinline__ bool aborted(Lds& L) {
+template <class LT>
+__device__ __forceinline__ bool aborted(LT& L) {
   return __hip_atomic_load(&L.abort_, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
 }
 // Has another workgroup of this launch failed?
-__device__ __forceinline__ bool grid_failed(const Ctl* ctl, const Lds& L) {
+template <class LT>
+__device__ __forceinline__ bool grid_failed(const Ctl* ctl, const LT& L) {
   return __hip_atomic_load(&ctl->error, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == L.epoch;
 }
 // The error word holds the epoch of the failing launch, so a failure that the
 // host has not cleared yet does not abort later launches.
-__device__ __forceinline__ void set_abort(Lds& L, Ctl* ctl) {
+template <class LT>
+__device__ __forceinline__ void set_abort(LT& L, Ctl* ctl) {
   __hip_atomic_store(&ctl->error, L.epoch, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __hip_atomic_store(&L.abort_, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -257,7 +275,8 @@ __device__ __forceinline__ int units_of(int units, int first, int G) {
 }
 
 // ---------------------------------------------------------------- input fetch
-__device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
+template <class LT>
+__device__ __forceinline__ bool poll_step(uint32_t& spins, LT& L, Ctl* ctl) {
   if (aborted(L)) return false;
   if (++spins > L.spin_max || ((spins & 255) == 0 && grid_failed(ctl, L))) {
     set_abort(L, ctl);
@@ -272,7 +291,8 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, Lds& L, Ctl* ctl) {
 // rounds of kFB words per lane, polling until every tag matches. A slice
 // whose items two waves share is fetched by both: the same values land twice.
 constexpr int kFB = 10;
-__device__ __forceinline__ void fetch_words(const OpDev& op, Lds& L, int lane, Ctl* ctl, uint32_t base_tag, int ob,
+template <class LT>
+__device__ __forceinline__ void fetch_words(const OpDev& op, LT& L, int lane, Ctl* ctl, uint32_t base_tag, int ob,
                                             int a0, int a1, int b0, int b1) {
   const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
@@ -326,7 +346,8 @@ __device__ __forceinline__ void early_issue(const OpDev& op, int lid, uint32_t b
 // Polls what was stale, writes the input into LDS buffer `ob`, then this
 // wave's L.early_seq = seq. Returns false (and writes nothing) if `wait` is
 // false and some word of this wave is not yet published.
-__device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, Lds& L, int ob,
+template <class LT>
+__device__ __forceinline__ bool early_finish(const OpDev& op, int lid, uint32_t base_tag, EarlyFetch& f, LT& L, int ob,
                                              Ctl* ctl, bool wait, uint32_t seq) {
   const uint64_t* in = sgpr_ptr(op.in_ll);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
@@ -383,7 +404,8 @@ __device__ __forceinline__ PrepRegs prep_regs(const OpDev& op) {  // (from the L
 constexpr int kSQ = 4;  // block sums of squares per lane per poll round
 // The RMSNorm scale of a GEMV's input: lane l adds the producers' block sums
 // l, l + 64, ... in order, then the wave sum (norm_scale_of).
-__device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd, Lds& L, int lane, Ctl* ctl,
+template <class LT>
+__device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd, LT& L, int lane, Ctl* ctl,
                                             uint32_t base_tag) {
   const int K = sgpr(op.K), nb = K >> 5;
   const uint64_t* sq = sgpr_ptr(op.in_ll) + K;
@@ -435,9 +457,9 @@ __device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd,
 // from 64 consecutive sources (the step program takes perm_hd % 64 == 0), so
 // the gather costs one uniform source index per run, recomputed at each use
 // (an empty asm keeps the compiler from holding 16 of them in registers).
-template <bool PERM>
+template <bool PERM, class LT>
 __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev* preps, int pi, float& scale,
-                                                 bool scale_due, Lds& L, int wave, int lane, Ctl* ctl,
+                                                 bool scale_due, LT& L, int wave, int lane, Ctl* ctl,
                                                  uint32_t base_tag, int ob, int sl) {
   // Each field of the prep is loaded (a scalar load) where it is used: the
   // pointer passes an empty asm before every use, so no field is held in
@@ -576,7 +598,8 @@ struct OpWork {
 };
 // Every field is assigned on every path (a partly assigned struct would be
 // kept in scratch memory, whose accesses count in vmcnt).
-__device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave, int wg, int G, int i) {
+template <class LT>
+__device__ __forceinline__ OpWork op_work_calc(const LT& L, int nops, int wave, int wg, int G, int i) {
   OpWork w;
   const bool past = i >= nops;
   const OpDev& o = L.opd[past ? 0 : i];
@@ -591,17 +614,20 @@ __device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave,
   const int U = w.S << w.qlog;  // items per unit
   const int T = nunits * U;
   // Batches are spread evenly over the waves, floor(B / kCW) each, the
-  // remaining B % kCW one more each, those first to the waves of SIMDs 2 and
-  // 3 (two compute waves each, beside the I/O waves; SIMDs 0 and 1 hold
-  // three): a wave's batches are rounds of its ring (each waits for the
-  // loads issued during the previous one), so the op takes as many rounds
-  // as its busiest wave has batches. Runs follow in wave order.
-  static_assert(kCW == 10, "the extra-batch order below assumes 3 + 3 + 2 + 2 compute waves per SIMD");
+  // remaining B % kCW one more each, those first to the compute waves of
+  // SIMDs 2 and 3 (wave v runs on SIMD v % 4; the I/O waves, the last two,
+  // sit on SIMDs 2 and 3, which so hold one compute wave fewer): a wave's
+  // batches are rounds of its ring (each waits for the loads issued during
+  // the previous one), so the op takes as many rounds as its busiest wave
+  // has batches. Runs follow in wave order.
+  constexpr int kCW = LT::kCW;
+  static_assert((kCW + kIW) % 4 == 0 && kIW == 2, "the extra-batch order assumes the I/O waves on SIMDs 2 and 3");
+  constexpr int n23 = 2 * ((kCW + kIW) / 4 - 1);  // compute waves on SIMDs 2 and 3
   const int B = (T + kRing - 1) / kRing;
   const int base = B / kCW, extra = B % kCW;
-  auto xrank = [](int v) {  // order of the extra batches: waves 2, 3, 6, 7, then 0, 1, 4, 5, 8, 9
+  auto xrank = [](int v) {  // order of the extra batches: (10 waves) 2, 3, 6, 7, then 0, 1, 4, 5, 8, 9
     const int sm = v & 3, sl = v >> 2;
-    return sm >= 2 ? (sm - 2) + 2 * sl : 4 + sm + 2 * sl;
+    return sm >= 2 ? (sm - 2) + 2 * sl : n23 + sm + 2 * sl;
   };
   int b0 = base * wave;
   for (int v = 0; v < wave; ++v) b0 += xrank(v) < extra ? 1 : 0;
@@ -619,16 +645,18 @@ __device__ __forceinline__ OpWork op_work_calc(const Lds& L, int nops, int wave,
 
 // Stage the records of op i (lanes 0 .. kCW-1 of the first I/O wave, one
 // per compute wave); read by the compute waves after the next barrier B.
-__device__ __forceinline__ void stage_work(Lds& L, int nops, int wg, int G, int i, int iol) {
+template <class LT>
+__device__ __forceinline__ void stage_work(LT& L, int nops, int wg, int G, int i, int iol) {
   asm volatile("" : "+v"(iol));  // lane tests formed here, not held from the kernel's start
-  if (iol < kCW) {
+  if (iol < LT::kCW) {
     const OpWork w = op_work_calc(L, nops, iol, wg, G, i);
     const int slot = i % kRecSlots;
     L.wrec[slot][iol] = WorkRec{w.t0, w.n, w.P, w.u0 | (w.s0 << 8) | (w.q0 << 16)};
     if (iol == 0) L.orec[slot] = OpRec{w.first, w.R, w.next, w.S | (w.qlog << 8)};
   }
 }
-__device__ __forceinline__ OpWork op_work(const Lds& L, int wave, int i) {
+template <class LT>
+__device__ __forceinline__ OpWork op_work(const LT& L, int wave, int i) {
   const int slot = i % kRecSlots;
   const WorkRec& r = L.wrec[slot][wave];
   const OpRec& o = L.orec[slot];
@@ -690,7 +718,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
   // stride 0, 4 GB of records, 32-bit data format (raw buffer loads)
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
 }
-__device__ __forceinline__ OpLd op_ld(const Lds& L, int i) {
+template <class LT>
+__device__ __forceinline__ OpLd op_ld(const LT& L, int i) {
   const OpDev& o = L.opd[i];
   OpLd d;
   d.sw = sgpr(o.mode) == BTF_GEMV_SWIGLU;
@@ -762,7 +791,8 @@ __device__ __forceinline__ void issue_entry(const OpLd& d, const LaneOff& lo, co
 // blocks): 64 q bytes, and per sub-block d/16 and -16 s (the dot returns
 // 16 * I; both conversions are exact). The 4 row groups of a wave read the
 // same addresses (LDS broadcasts).
-__device__ __forceinline__ void load_act(const Lds& L, int ob, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
+template <class LT>
+__device__ __forceinline__ void load_act(const LT& L, int ob, int s, int l16, uint32_t (&aq)[16], float (&ad)[2],
                                          int (&an)[2]) {
   const int blk = 2 * (s * 16 + l16);
   const uint2* p = reinterpret_cast<const uint2*>(&L.act[ob][blk * kWordsPerBlock]);  // 8-byte aligned
@@ -876,7 +906,7 @@ __device__ __forceinline__ bool sum_lanes(int l16) {
 // per-batch bookkeeping (addresses, partial-sum slots, the unit's count, the
 // activation reload at a new slice) is uniform and done once per batch.
 template <bool kFull>
-__device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
+__device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first, int wave, int lane, int wg, int G, Ctl* ctl,
                                               uint32_t base_tag) {
   const int l16 = lane & 15, grp = lane >> 4;
   const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
@@ -908,7 +938,7 @@ __device__ __forceinline__ void compute_waves(Lds& L, int nops, int first, int w
       const int pf = sgpr(L.opd[opi].prep_flags);
       const bool norm = (pf & 1) != 0, perm = (pf & 2) != 0;
       auto mine = [&](auto pm) {
-        for (int sl = wave; sl < sgpr(L.opd[opi].K) / kSliceVals; sl += kCW) {
+        for (int sl = wave; sl < sgpr(L.opd[opi].K) / kSliceVals; sl += Lds<kFull>::kCW) {
           fetch_prep_slice<decltype(pm)::value>(L.opd[opi], sgpr_ptr(L.preps), sgpr(L.opd[opi].prep), scale,
                                                 norm && sl == wave, L, wave, lane, ctl, base_tag, ob, sl);
           asm volatile("" ::: "memory");  // the image words before the flag (LDS ops of a wave complete in order)
@@ -1156,7 +1186,8 @@ __device__ __forceinline__ void io_quantize(const OpDev& op, int wg, int G, int 
 // Write-after-read guard: the version of the output vector this op replaces
 // may still be needed by a workgroup that has not fetched the input of op
 // `war_op` yet; wait until all G have (rd_cnt counts them, G per launch).
-__device__ __forceinline__ void wait_readers(int war_op, const uint32_t* rd_cnt, int G, Lds& L, Ctl* ctl) {
+template <class LT>
+__device__ __forceinline__ void wait_readers(int war_op, const uint32_t* rd_cnt, int G, LT& L, Ctl* ctl) {
   if (war_op < 0) return;
   const uint32_t want = L.epoch * (uint32_t)G;
   uint32_t spins = 0;
@@ -1176,8 +1207,10 @@ __device__ __forceinline__ void wait_readers(int war_op, const uint32_t* rd_cnt,
 // applies the mode (old value: the LDS carry, or the LL word of the previous
 // version, loaded one unit ahead) and publishes. Returns each counter to 0
 // for the next op.
-__device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int G, int iol, uint32_t base_tag,
+template <bool kFull, class LT>
+__device__ __forceinline__ void io_publish(const OpDev& op, LT& L, int wg, int G, int iol, uint32_t base_tag,
                                            Ctl* ctl) {
+  asm volatile("" : "+v"(iol));  // lane values formed here, not held from the kernel's start
   const int half = iol >> 5, j = iol & 31, nhalves = kIW * 2;
   const int first = first_unit(sgpr(op.rot), wg, G);
   const int nunits = units_of(sgpr(op.units), first, G);
@@ -1195,7 +1228,7 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
     return (old_ll && ui < nunits && row < N) ? ll_load(old + row) : ((uint64_t)told << 32);
   };
   uint64_t ov = old_word(half);
-  const bool pick = sgpr(op.argmax);
+  const bool pick = kFull && sgpr(op.argmax);
   uint64_t best = 0;  // the largest pick key of the rows this lane published
   for (int ui = half; ui < nunits; ui += nhalves) {
     {
@@ -1206,14 +1239,15 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
       for (;;) {
         uint32_t done = 0;
 #pragma unroll
-        for (int w = 0; w < kCW; ++w) done += __hip_atomic_load(&L.ucnt[w][ui], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        for (int w = 0; w < LT::kCW; ++w)
+          done += __hip_atomic_load(&L.ucnt[w][ui], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (done == items || !poll_step(spins, L, ctl)) break;
         __builtin_amdgcn_s_sleep(3);
       }
       __builtin_amdgcn_s_setprio(3);
     }
     asm volatile("" ::: "memory");
-    if (j < kCW) __hip_atomic_store(&L.ucnt[j][ui], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    if (j < LT::kCW) __hip_atomic_store(&L.ucnt[j][ui], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int unit = first + ui * G;
     const int row = unit * 32 + j;
     const bool valid = row < N;
@@ -1261,7 +1295,8 @@ __device__ __forceinline__ void io_publish(const OpDev& op, Lds& L, int wg, int 
 // op's input, finish the early fetch.
 // The program's greedy pick (workgroup 0's first I/O wave, after its last
 // op): the largest of the G workgroups' keys, polled from their LL words.
-__device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int lane, Ctl* ctl, uint32_t base_tag) {
+template <class LT>
+__device__ __forceinline__ void io_pick(const HeadDev* head, LT& L, int G, int lane, Ctl* ctl, uint32_t base_tag) {
   const cptr<HeadDev> h = as_const(head);
   const uint64_t* parts = sgpr_ptr(h->parts);
   const uint32_t tag = base_tag + sgpr((int)h->tag);
@@ -1308,7 +1343,7 @@ __device__ __forceinline__ void io_pick(const HeadDev* head, Lds& L, int G, int 
 // op's input (and publish its pick key), finish the early fetch. Prologue ops
 // (quantize, embedding) run before the first GEMV.
 template <bool kFull>
-__device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
+__device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
                                          uint32_t base_tag) {
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
@@ -1334,7 +1369,7 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
     // still being computed. Waiting for these loads later would also wait
     // for the op's own output stores to complete (vmcnt counts both).
     if (early) early_done = early_finish(L.opd[nx], iol, base_tag, ef, L, nx & 1, ctl, false, (uint32_t)nx + 1);
-    io_publish(op, L, wg, G, iol, base_tag, ctl);
+    io_publish<kFull>(op, L, wg, G, iol, base_tag, ctl);
     lds_barrier();  // B: every compute wave is done with the op's input
     const bool io0 = sgpr(iol >> 6) == 0;  // the first I/O wave
     if (sgpr(op.count_reads) && io0 && first_lane(iol))
@@ -1357,10 +1392,11 @@ __device__ __forceinline__ void io_waves(Lds& L, int nops, Ctl* ctl, uint32_t* r
 // lookup or a greedy pick; the plain one (a chain of GEMVs on Q8 inputs)
 // without that code.
 template <bool kFull>
-__global__ void __launch_bounds__(kThreads) step_kernel(const OpDev* __restrict__ ops, int nops, int first_gemv,
+__global__ void __launch_bounds__(threads_of<kFull>()) step_kernel(const OpDev* __restrict__ ops, int nops, int first_gemv,
                                                         Ctl* ctl, uint32_t* rd_cnt, const PrepDev* __restrict__ preps,
                                                         const HeadDev* __restrict__ head) {
-  __shared__ Lds L;
+  constexpr int kCW = cw_of<kFull>(), kThreads = threads_of<kFull>();
+  __shared__ Lds<kFull> L;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wg = blockIdx.x, G = gridDim.x;
   // stage the program in LDS
@@ -1957,7 +1993,8 @@ int step_check_residency(const DevState& ds) {
   if (!coop) return fail(BTF_ERR_DEVICE, "step: the device does not support cooperative launches");
   int per_cu = 0;
   for (const void* k : {reinterpret_cast<const void*>(step_kernel<false>), reinterpret_cast<const void*>(step_kernel<true>)}) {
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, kThreads, 0) != hipSuccess)
+    const int threads = k == reinterpret_cast<const void*>(step_kernel<true>) ? threads_of<true>() : threads_of<false>();
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, k, threads, 0) != hipSuccess)
       return fail(BTF_ERR_LAUNCH, "step: occupancy query failed");
     if (per_cu < 1) return fail(BTF_ERR_LAUNCH, "step: the step kernel does not fit on a CU");
   }
@@ -1973,7 +2010,7 @@ int step_launch(StepProgram* P, hipStream_t st) {
   const hipError_t e =
       hipLaunchCooperativeKernel(P->full ? reinterpret_cast<const void*>(step_kernel<true>)
                                          : reinterpret_cast<const void*>(step_kernel<false>),
-                                 dim3(P->G), dim3(kThreads), args, 0, st);
+                                 dim3(P->G), dim3(P->full ? threads_of<true>() : threads_of<false>()), args, 0, st);
   if (e != hipSuccess) return fail(BTF_ERR_LAUNCH, std::string("step kernel: ") + hipGetErrorString(e));
   return launch_status("step_kernel");
 }
