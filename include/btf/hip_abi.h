@@ -234,10 +234,10 @@ int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls);
  *  - BTF_STEP_GEMV: `gemv` as in btf_hip_step_create, its input first put
  *    through launch_prep's pipeline (src/cuda/kernels.cuh:40-43): RMSNorm *
  *    normw (NULL: none, eps its epsilon), then the transform hx (block 0:
- *    none; a power of two <= 1024; perm_hd * perm_nk * perm_rep == K when
- *    perm_rep > 1; signs NULL or [K]), then Q8_0. With a norm or transform
- *    the input vector's length must equal K. Bit-identical to launch_prep +
- *    launch_gemv.
+ *    none; a power of two <= 1024; perm_hd * perm_nk * perm_rep == K and
+ *    perm_hd % 64 == 0 when perm_rep > 1; signs NULL or [K]), then Q8_0.
+ *    With a norm or transform the input vector's length must equal K.
+ *    Bit-identical to launch_prep + launch_gemv.
  *  - BTF_STEP_EMBED: vector `vec` (length E, a multiple of 1024) = row
  *    *d_tok of the packed table (table_codes [V][E/4], table_scales
  *    [V][E/128], device or mapped host memory) with the inverse transform hx
