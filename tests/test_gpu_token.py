@@ -230,3 +230,48 @@ def test_whole_token_one_layer_pieces_vs_oracle(hip, oracle):
             want = oracle.gemv(W[0], W[1], K, q, d, s_, y=old[None, :].copy() if mode == "add" else None,
                                add=mode == "add")[0]
         assert_close_1e3(got, want, f"op {k}")
+
+
+@pytest.mark.parametrize("block", [2, 4, 8, 16, 32, 64, 128, 256, 512, 1024])
+def test_step_prep_every_transform_block(hip, oracle, block):
+    """Each transform block size through the step program's prep (the
+    strided slice layout puts stages len = 1..32 across lanes and 64..512 in
+    the lane, so small blocks use only the cross-lane stages): a two-GEMV
+    program -- the first with RMSNorm + signs + FWHT, the second with the
+    tiled -> grouped gather + FWHT, over a 3-slice input (K = 3072) so that
+    the slices land on different waves -- bit-exact with launch_prep +
+    launch_gemv, and each GEMV within the oracle's bars."""
+    torch = _torch()
+    rng = np.random.default_rng(100 + block)
+    K, N1, N2 = 3072, 3072, 640
+    G = hip.GemvMode
+    W1 = random_mat(oracle, rng, N1, K, scale=0.03)
+    W2 = random_mat(oracle, rng, N2, N1, scale=0.03)
+    normw = (1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32)
+    sg = np.where(rng.random(K) < 0.5, -1.0, 1.0).astype(np.float32)
+    x0 = rng.standard_normal(K).astype(np.float32)
+    keep = [dev(a) for a in (W1[0], W1[1], W2[0], W2[1], normw, sg)]
+    c1, s1, c2, s2, dnw, dsg = keep
+    hx1 = hip.Hx(block=block, signs=dsg)
+    hx2 = hip.Hx(block, 64, 12, 4)  # gather: hd 64, nk 12, rep 4 -> 3072
+    ops = [hip.StepGemv(G.kStore, K, N1, c1.data_ptr(), s1.data_ptr(), 0, 1, normw=dnw, eps=1e-6, hx=hx1),
+           hip.StepGemv(G.kStore, N1, N2, c2.data_ptr(), s2.data_ptr(), 1, 2, hx=hx2)]
+
+    def vectors():
+        return [dev(x0), torch.zeros(N1, dtype=torch.float32, device="cuda"),
+                torch.zeros(N2, dtype=torch.float32, device="cuda")]
+
+    t = vectors()
+    prog = hip.StepProgram([hip.StepVec(K, t[0]), hip.StepVec(N1, t[1]), hip.StepVec(N2, t[2])], ops)
+    prog.launch(stream())
+    torch.cuda.synchronize()
+    assert prog.error() == 0
+    prog.close()
+    s = vectors()
+    run_ops_sequential(hip, ops, s)
+    for name, a, b in zip(("x", "y1", "y2"), t, s):
+        assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32)), f"block {block}: {name}"
+    q, d, s_, _ = oracle.prep(x0[None, :], normw, 1e-6, block, 0, 0, 0, sg)
+    assert_close_1e3(host(t[1]), oracle.gemv(W1[0], W1[1], K, q, d, s_)[0], f"block {block}: GEMV 1")
+    q, d, s_, _ = oracle.prep(host(t[1])[None, :], None, 0.0, block, 64, 12, 4, None)
+    assert_close_1e3(host(t[2]), oracle.gemv(W2[0], W2[1], N1, q, d, s_)[0], f"block {block}: GEMV 2")
