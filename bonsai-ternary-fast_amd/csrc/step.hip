@@ -282,8 +282,7 @@ __device__ __forceinline__ bool poll_step(uint32_t& spins, LT& L, Ctl* ctl) {
     set_abort(L, ctl);
     return false;
   }
-  __builtin_amdgcn_s_sleep(1);
-  return true;
+  return true;  // (no sleep: a poll round is paced by its own loads' round trip)
 }
 
 // Fetch LL words [a0, a1) and [b0, b1) of an op's input (its Q8 words, tag = the input
@@ -945,10 +944,15 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
           __hip_atomic_store(&L.sready[ob][sl], (uint32_t)opi + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         }
       };
+      // raised priority: every wave with items of the op waits for these
+      // slices, so their instructions go before those of the I/O waves and
+      // of the waves that poll
+      __builtin_amdgcn_s_setprio(2);
       if (perm)
         mine(std::true_type{});
       else
         mine(std::false_type{});
+      __builtin_amdgcn_s_setprio(0);
     }
     const OpWork cur = op_work(L, wave, opi);
     if (cur.n > 0) {
@@ -1232,9 +1236,8 @@ __device__ __forceinline__ void io_publish(const OpDev& op, LT& L, int wg, int G
   uint64_t best = 0;  // the largest pick key of the rows this lane published
   for (int ui = half; ui < nunits; ui += nhalves) {
     {
-      // polled at normal priority and sparsely: the compute waves on the
-      // same SIMDs are producing these items
-      __builtin_amdgcn_s_setprio(0);
+      // polled sparsely: the compute waves on the same SIMDs are producing
+      // these items
       uint32_t spins = 0;
       for (;;) {
         uint32_t done = 0;
@@ -1242,9 +1245,8 @@ __device__ __forceinline__ void io_publish(const OpDev& op, LT& L, int wg, int G
         for (int w = 0; w < LT::kCW; ++w)
           done += __hip_atomic_load(&L.ucnt[w][ui], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         if (done == items || !poll_step(spins, L, ctl)) break;
-        __builtin_amdgcn_s_sleep(3);
+        __builtin_amdgcn_s_sleep(1);
       }
-      __builtin_amdgcn_s_setprio(3);
     }
     asm volatile("" ::: "memory");
     if (j < LT::kCW) __hip_atomic_store(&L.ucnt[j][ui], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -1430,12 +1432,10 @@ __global__ void __launch_bounds__(threads_of<kFull>()) step_kernel(const OpDev* 
   if (wave < kCW)
     compute_waves<kFull>(L, nops, first_gemv, wave, lane, wg, G, ctl, base_tag);
   else {
-    // The I/O waves' epilogue of an op is on the chain's critical path while
-    // the compute waves already run the next op's dot products on the same
-    // SIMDs: their instructions issue first (the waits in between sleep).
-    __builtin_amdgcn_s_setprio(3);
+    // (at the compute waves' priority: raised above them, the I/O waves'
+    // polls took issue slots from the preps of whole-token programs, 3.41
+    // against 3.23 ms per token, and gained nothing for a plain chain)
     io_waves<kFull>(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
-    __builtin_amdgcn_s_setprio(0);
   }
 
   // ---------------- end of step: count the workgroup out; the last one to
