@@ -75,3 +75,32 @@ def test_no_kernel_uses_scratch_or_spills():
                            f"VGPRs {k.get('VGPRs')}")
     assert n > 0, "no kernel resource remarks were parsed"
     assert not bad, "kernels with scratch or spills:\n" + "\n".join(bad)
+
+
+def _assembly(src):
+    flags, per_file = _flags()
+    stem = os.path.splitext(os.path.basename(src))[0]
+    cmd = [HIPCC] + flags + per_file.get(stem, []) + ["--cuda-device-only", "-S", os.path.join(PKG, src), "-o", "-"]
+    p = subprocess.run(cmd, capture_output=True, text=True, cwd=PKG)
+    assert p.returncode == 0, f"{src} does not compile:\n{p.stderr[-2000:]}"
+    return p.stdout
+
+
+@pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not available")
+def test_no_kernel_issues_flat_memory_instructions():
+    """No kernel reaches memory through a flat (generic) instruction. A flat
+    access counts in both the vector-memory and the LDS/scalar counters, so a
+    wait for its result (or any LDS wait after it) also waits for every
+    global load issued before it -- in the step kernel, the weight stream in
+    flight. Pointers that come back generic from LDS are cast to the global
+    or constant address space where they are used."""
+    srcs = _sources()
+    with ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        asm = dict(zip(srcs, ex.map(_assembly, srcs)))
+    bad = []
+    for src, text in asm.items():
+        for line in text.splitlines():
+            s = line.strip()
+            if s.startswith(("flat_load", "flat_store", "flat_atomic")):
+                bad.append(f"{src}: {s}")
+    assert not bad, "flat memory instructions:\n" + "\n".join(bad[:20])
