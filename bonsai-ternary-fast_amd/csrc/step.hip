@@ -720,15 +720,21 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
 template <class LT>
 __device__ __forceinline__ OpLd op_ld(const LT& L, int i) {
   const OpDev& o = L.opd[i];
-  OpLd d;
-  d.sw = sgpr(o.mode) == BTF_GEMV_SWIGLU;
+  // Every field is read before any is tested, so the reads are in flight
+  // together (one LDS round trip; reading the up matrix only for a swiglu
+  // would make it a second, and this sits on the critical path of an op).
+  const int mode = sgpr(o.mode);
   const uint8_t* c = sgpr_ptr(o.codes);
   const uint16_t* sc = sgpr_ptr(o.scales);
+  const uint8_t* uc = sgpr_ptr(o.up_codes);
+  const uint16_t* us = sgpr_ptr(o.up_scales);
+  const uint32_t K = (uint32_t)sgpr(o.K), N = (uint32_t)sgpr(o.N);
+  OpLd d;
+  d.sw = mode == BTF_GEMV_SWIGLU;
   d.clo = rsrc(c);
   d.slo = rsrc(sc);
-  d.chi = rsrc(d.sw ? sgpr_ptr(o.up_codes) : c);
-  d.shi = rsrc(d.sw ? sgpr_ptr(o.up_scales) : sc);
-  const uint32_t K = (uint32_t)sgpr(o.K), N = (uint32_t)sgpr(o.N);
+  d.chi = rsrc(d.sw ? uc : c);
+  d.shi = rsrc(d.sw ? us : sc);
   d.rowc = K >> 2;
   d.rows = K >> 6;
   d.lastc = (N - 4) * d.rowc;
@@ -993,8 +999,8 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       }
     }
     }
+    OpLd ld_cur = op_ld(L, opi);  // (its reads first: in flight with op_work's)
     const OpWork cur = op_work(L, wave, opi);
-    OpLd ld_cur = op_ld(L, opi);
     LaneOff lo_cur = lane_off(ld_cur, l16, grp);
     const int U = cur.S << cur.qlog;  // items per unit
     BPos cp{cur.u0, cur.s0, cur.q0};  // the batch being consumed
@@ -1043,11 +1049,11 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       // the last batch refills with the next op's first batch (past the
       // program's end: this op's matrices again). Its addresses are formed
       // only here, so they hold no registers through the op's other batches.
+      // (read unconditionally -- past the program's end this op's own
+      // descriptor again -- so that no branch splits the reads)
+      ld_cur = op_ld(L, cur.next < nops ? cur.next : opi);
       const OpWork nw = op_work(L, wave, cur.next);
-      if (cur.next < nops) {
-        ld_cur = op_ld(L, cur.next);
-        lo_cur = lane_off(ld_cur, l16, grp);
-      }
+      lo_cur = lane_off(ld_cur, l16, grp);
       run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nw.first, G, BPos{nw.u0, nw.s0, nw.q0}), cp, true);
     }
     lds_barrier();  // B: every wave is done with the op
