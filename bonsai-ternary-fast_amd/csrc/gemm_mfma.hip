@@ -41,6 +41,7 @@ namespace {
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
+
 struct MfmaArgs {
   const uint8_t* codes[3];
   const uint16_t* scales[3];
@@ -940,22 +941,31 @@ __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
         const uint32_t hi = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> (sh + 2)) & 0x03030303u);
         bfrag[j] = (long)(((uint64_t)hi << 32) | lo);
       }
+      // every MFMA of the sub-block first, into its own registers, then the
+      // scaling: the matrix core runs the next products while the vector ALU
+      // converts the earlier ones (one result register set, reused, would
+      // make each MFMA wait for the conversions of the one before)
+      v4i I[MW][2];
+#pragma unroll
+      for (int mt = 0; mt < MW; ++mt) {
+        const int r = 16 * MW * wm + 16 * mt + li;
+        const long afrag = *reinterpret_cast<const long*>(stg + r * 128 + 16 * ((2 * sb + (t >> 1)) ^ (r & 7)) +
+                                                          8 * (t & 1));
+#pragma unroll
+        for (int j = 0; j < 2; ++j) I[mt][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], zero, 0, 0, 0);
+      }
 #pragma unroll
       for (int mt = 0; mt < MW; ++mt) {
         const int mr = 16 * MW * wm + 16 * mt;
-        const int r = mr + li;
-        const long afrag = *reinterpret_cast<const long*>(stg + r * 128 + 16 * ((2 * sb + (t >> 1)) ^ (r & 7)) +
-                                                          8 * (t & 1));
         float dv[4];
 #pragma unroll
         for (int rr = 0; rr < 4; ++rr) dv[rr] = dst[(mr + 4 * t + rr) * 4 + sb];
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], zero, 0, 0, 0);
+        for (int j = 0; j < 2; ++j)
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr)
-            blk[j][mt][rr] = sb == 0 ? dv[rr] * (float)I[rr] : fmaf(dv[rr], (float)I[rr], blk[j][mt][rr]);
-        }
+            blk[j][mt][rr] =
+                sb == 0 ? dv[rr] * (float)I[mt][j][rr] : fmaf(dv[rr], (float)I[mt][j][rr], blk[j][mt][rr]);
       }
     }
 #pragma unroll
@@ -1078,7 +1088,7 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
     // the LDS-direct ring loads d in 16-byte pieces
     if ((reinterpret_cast<uintptr_t>(act.d) & 15) == 0) {
       if (wide)
-        by_mode_pf2<4, 2>(mode, a, dim3(tiles, (nb + 127) / 128), st);  // 41 KB: 3 workgroups per CU
+        by_mode_pf2<4, 2>(mode, a, dim3(tiles, (nb + 127) / 128), st);  // 41 KB; 190 VGPRs: 2 workgroups per CU
       else
         by_mode_pf2<2, 3>(mode, a, dim3(tiles, (nb + 63) / 64), st);  // 34 KB: 4 workgroups per CU
       return launch_status("gemm_pf2_kernel");
