@@ -402,10 +402,14 @@ __device__ __forceinline__ PrepRegs prep_regs(const OpDev& op) {  // (from the L
 
 constexpr int kSQ = 4;  // block sums of squares per lane per poll round
 // The RMSNorm scale of a GEMV's input: lane l adds the producers' block sums
-// l, l + 64, ... in order, then the wave sum (norm_scale_of).
-template <class LT>
+// l, l + 64, ... in order, then the wave sum (norm_scale_of). `again` runs
+// in every poll round before the stale words are loaded again: the caller
+// re-loads its own stale input words there, so they travel with the sums
+// (a producer publishes a unit's values before its sum of squares), and
+// once the sums are in, the values usually are too -- no further round trip.
+template <class LT, class F>
 __device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd, LT& L, int lane, Ctl* ctl,
-                                            uint32_t base_tag) {
+                                            uint32_t base_tag, F&& again) {
   const int K = sgpr(op.K), nb = K >> 5;
   const uint64_t* sq = sgpr_ptr(op.in_ll) + K;
   const uint32_t tin = base_tag + sgpr(op.in_tag);
@@ -426,6 +430,7 @@ __device__ __forceinline__ float prep_scale(const OpDev& op, const PrepRegs& pd,
         pending |= ((uint32_t)(lo[b] >> 32) != tin || (uint32_t)(hi[b] >> 32) != tin) ? (1u << b) : 0u;
       if (__builtin_amdgcn_ballot_w64(pending != 0) == 0) break;
       if (!poll_step(spins, L, ctl)) break;
+      again();
 #pragma unroll
       for (int b = 0; b < kSQ; ++b)
         if (pending & (1u << b)) {
@@ -495,8 +500,12 @@ __device__ __forceinline__ void fetch_prep_slice(const OpDev& op, const PrepDev*
 #pragma unroll
     for (int i = 0; i < 16; ++i) pre[i] = signs[c + 64 * i + lane];
   }
-  if (scale_due) scale = prep_scale(op, pd, L, lane, ctl, base_tag);
   const uint32_t tin = base_tag + sgpr(op.in_tag);
+  if (scale_due)
+    scale = prep_scale(op, pd, L, lane, ctl, base_tag, [&]() {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) w[i] = ll_load(in + src(i));  // (all of them: no mask to hold)
+    });
   uint32_t spins = 0;
   for (;;) {
     uint32_t pending = 0;
