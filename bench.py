@@ -456,12 +456,18 @@ def run_token(S: Setup, hip, torch, layers, steps, warmup, prep="full", traffic_
             outs.append([t.cpu().numpy().copy() for t in (T.res, T.qkv, T.h, T.logits, T.tok, T.pos)])
         if prog.error():
             raise SystemExit("whole-token program reported a timeout")
-        for name, a, b in zip(("res", "qkv", "h", "logits", "token", "pos"), *outs):
-            if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
-                raise SystemExit(f"whole-token program != op-by-op launches ({name})")
-        if not np.isfinite(outs[0][3]).all():
-            raise SystemExit("whole-token logits are not finite")
-        log(f"whole-token program vs op-by-op launches: bit-exact (token {int(outs[0][4][0])})")
+        if prep != "full" and not all(np.isfinite(a).all() for a in outs[0][:4]):
+            # without the RMSNorms the residual grows layer by layer until it
+            # overflows; the quantize of non-finite values is not a defined
+            # result to compare (a measurement mode only)
+            log(f"whole-token program (prep {prep}): the residual overflows without norms; not compared")
+        else:
+            for name, a, b in zip(("res", "qkv", "h", "logits", "token", "pos"), *outs):
+                if not np.array_equal(a.view(np.uint32), b.view(np.uint32)):
+                    raise SystemExit(f"whole-token program != op-by-op launches ({name})")
+            if not np.isfinite(outs[0][3]).all():
+                raise SystemExit("whole-token logits are not finite")
+            log(f"whole-token program vs op-by-op launches: bit-exact (token {int(outs[0][4][0])})")
         T.reset()
         ms = time_program(hip, torch, prog, steps, warmup)
     finally:

@@ -104,7 +104,9 @@ __device__ __forceinline__ int half32_sum(int v) {
   return (int)r[0] + (int)r[1];
 }
 __device__ __forceinline__ int q8_half(float v, float& d, int& s) {
-  const float amax = half32_max(fabsf(v));
+  // (the running max starts at 0, as the q8 kernel's and the CPU's: a NaN
+  // value never becomes the block's amax)
+  const float amax = half32_max(fmaxf(0.f, fabsf(v)));
   float dd = h2f(f2h_bits(amax / 127.0f));
   if (amax == 0.f) dd = copysignf(0.f, __shfl(v, 31, 32));  // all 32 lanes of the half take this branch
   d = dd;

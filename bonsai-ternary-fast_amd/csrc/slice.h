@@ -180,7 +180,9 @@ __device__ __forceinline__ void q8_pair(const float (&v)[16], uint32_t (&qw)[4],
 // the all-zero case reads the sign of value 31, lane 7's v[3], through the
 // half-row mirror). Arithmetic of q8_pair.
 __device__ __forceinline__ uint32_t q8_oct(const float (&v)[4], float& d, int& s) {
-  float amax = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  float amax = 0.f;  // (from 0, as q8_pair: a NaN value never becomes the amax)
+#pragma unroll
+  for (int b = 0; b < 4; ++b) amax = fmaxf(amax, fabsf(v[b]));
   amax = fmaxf(amax, lane_xor<1>(amax));
   amax = fmaxf(amax, lane_xor<2>(amax));
   amax = fmaxf(amax, dpp_f<0x141>(amax));  // row_half_mirror: the other quad of the 8

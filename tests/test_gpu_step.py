@@ -541,6 +541,50 @@ def test_step_add_after_swiglu_into_the_same_vector(hip, oracle):
     prog.close()
 
 
+def test_step_nan_values_quantize_as_the_q8_kernel(hip, oracle):
+    """NaN values in a GEMV input: the Q8 of a block drops them (its running
+    max starts at 0, as in the q8 kernel and on the CPU, so a NaN never
+    becomes the amax; an all-NaN block is an all-zero one). Both of the step
+    program's producer-side quantizes: a user vector with NaNs (the
+    prologue's), and the NaN outputs of GEMV rows with NaN scales that the
+    next GEMV reads (the epilogue's). Bit-exact against the op-by-op
+    launches, and the second GEMV's outputs finite."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(91)
+    K0, N0, N1 = 1024, 2048, 1024
+    x0 = rng.standard_normal(K0).astype(np.float32)
+    x0[0:32] = np.nan  # an all-NaN block
+    x0[100] = np.nan   # one NaN among finite values
+    c0, s0 = random_mat(oracle, rng, N0, K0, scale=0.03)
+    s0 = s0.copy()
+    s0[64:96] = 0x7E00  # one whole output block of NaN rows
+    s0[200, 3] = 0x7E00  # and one NaN row among finite ones
+    W0 = Mat(dev(c0), dev(s0), N0, K0, c0, s0)
+    W1 = host_mat(oracle, rng, N1, N0)
+    ops = [hip.StepGemv(G.kStore, K0, N0, W0.codes, W0.scales, 0, 1),
+           hip.StepGemv(G.kStore, N0, N1, W1.codes, W1.scales, 1, 2)]
+
+    def vectors():
+        t = [dev(x0), torch.zeros(N0, dtype=torch.float32, device="cuda"),
+             torch.zeros(N1, dtype=torch.float32, device="cuda")]
+        return [hip.StepVec(int(v.numel()), v) for v in t], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    prog.launch(stream())
+    _torch().cuda.synchronize()
+    assert prog.error() == 0
+    prog.close()
+    _, s = vectors()
+    run_sequential(hip, ops, s)
+    h1 = host(s[1])
+    assert np.isnan(h1[64:96]).all() and np.isnan(h1[200]) and np.isfinite(h1[96:200]).all()
+    for name, a, b in zip(("x", "a", "y"), t, s):
+        assert np.array_equal(host(a).view(np.uint32), host(b).view(np.uint32)), name
+    assert np.isfinite(host(t[2])).all()
+
+
 def test_step_invalid_programs(hip):
     torch = _torch()
     G = hip.GemvMode

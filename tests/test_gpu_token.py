@@ -232,6 +232,38 @@ def test_whole_token_one_layer_pieces_vs_oracle(hip, oracle):
         assert_close_1e3(got, want, f"op {k}")
 
 
+def test_step_prep_nan_input_quantizes_as_launch_prep(hip, oracle):
+    """A NaN in a prepped GEMV's input: the transform spreads it over its
+    1024-value block, whose Q8 blocks are then all NaN and quantize to zero
+    (the running max starts at 0, as in launch_prep). With the RMSNorm the
+    whole input is NaN (the scale is). Bit-exact against launch_prep +
+    launch_gemv, with finite outputs."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(92)
+    K, N = 3072, 1024
+    x = rng.standard_normal(K).astype(np.float32)
+    x[1500] = np.nan
+    W = random_mat(oracle, rng, N, K, scale=0.03)
+    Wd = (dev(W[0]), dev(W[1]))
+    signs = dev(np.where(rng.random(K) < 0.5, -1.0, 1.0).astype(np.float32))
+    normw = dev((1.0 + 0.1 * rng.standard_normal(K)).astype(np.float32))
+    for norm in (None, normw):
+        ops = [hip.StepGemv(G.kStore, K, N, *Wd, 0, 1, normw=norm, eps=1e-6, hx=hip.Hx(block=1024, signs=signs))]
+        vec = lambda: [dev(x), torch.zeros(N, dtype=torch.float32, device="cuda")]
+        t = vec()
+        prog = hip.StepProgram([hip.StepVec(int(v.numel()), v) for v in t], ops)
+        prog.launch(stream())
+        torch.cuda.synchronize()
+        assert prog.error() == 0
+        prog.close()
+        s = vec()
+        run_ops_sequential(hip, ops, s)
+        got, want = host(t[1]), host(s[1])
+        assert np.isfinite(got).all(), f"norm={norm is not None}"
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"norm={norm is not None}"
+
+
 @pytest.mark.parametrize("block", [2, 4, 8, 16, 32, 64, 128, 256, 512, 1024])
 def test_step_prep_every_transform_block(hip, oracle, block):
     """Each transform block size through the step program's prep (the
