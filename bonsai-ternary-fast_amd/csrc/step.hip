@@ -104,7 +104,7 @@ struct OpDev {
   uint8_t early;        // 1: the I/O waves fetch this op's input during the previous op
   uint8_t carry_in;     // 1: add-mode old values come from the previous op's epilogue (LDS carry)
   uint8_t carry_out;    // 1: the epilogue keeps its outputs in the LDS carry for the next op
-  uint8_t count_reads;  // 1: count the workgroups that have fetched this op's input
+  uint8_t count_reads;  // 1: record the workgroup's progress after the op (a later write-after-read guard waits for it)
   uint8_t out_sq;       // 1: also publish each 32-value block's sum of squares (a later op normalizes it)
   uint8_t argmax;       // 1: the program's greedy pick reads this op's output
   uint8_t prep_flags;   // with a prep: bit 0 RMSNorm, bit 1 the tiled -> grouped gather
@@ -1204,13 +1204,34 @@ __device__ __forceinline__ void io_quantize(const OpDev& op, int wg, int G, int 
 
 // Write-after-read guard: the version of the output vector this op replaces
 // may still be needed by a workgroup that has not fetched the input of op
-// `war_op` yet; wait until all G have (rd_cnt counts them, G per launch).
+// `war_op` yet; wait until all G have. Each workgroup records its progress in
+// a word of its own (prog[wg] = the tag of the last op with count_reads whose
+// barrier B it has passed; tags only grow, launch after launch), so the wait
+// reads G words (4 per lane) instead of a counter that
+// G workgroups increment: same-address atomics from every workgroup
+// serialize in the memory system, and the count then completes microseconds
+// after the last workgroup passed.
 template <class LT>
-__device__ __forceinline__ void wait_readers(int war_op, const uint32_t* rd_cnt, int G, LT& L, Ctl* ctl) {
+__device__ __forceinline__ void wait_readers(int war_op, const uint32_t* prog, int G, LT& L, Ctl* ctl,
+                                             uint32_t base_tag, int lane) {
   if (war_op < 0) return;
-  const uint32_t want = L.epoch * (uint32_t)G;
+  // (the target and this lane's words in vector registers: scalar registers
+  // are short in the I/O waves)
+  uint32_t want = base_tag + (uint32_t)war_op + 1;
+  const uint32_t* mine = prog + lane;
+  asm volatile("" : "+v"(want), "+v"(mine));
   uint32_t spins = 0;
-  while ((int32_t)(ctl_load(rd_cnt + war_op) - want) < 0 && !aborted(L)) {
+  for (;;) {
+    // lane l: workgroups l, l + 64, ... (the buffer has 256 words; G <= 256);
+    // sign bits instead of compares: no lane masks held in scalar registers
+    uint32_t behind = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t v = __hip_atomic_load((const __attribute__((address_space(1))) uint32_t*)(mine + 64 * k),
+                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      behind |= (v - want) & (uint32_t)(lane + 64 * k - G);  // sign: behind, and a workgroup of the grid
+    }
+    if (__builtin_amdgcn_ballot_w64((int32_t)behind < 0) == 0 || aborted(L)) break;
     if (++spins > L.spin_max || ((spins & 255) == 0 && grid_failed(ctl, L))) {
       set_abort(L, ctl);
       break;
@@ -1360,7 +1381,7 @@ __device__ __forceinline__ void io_pick(const HeadDev* head, LT& L, int G, int l
 // op's input (and publish its pick key), finish the early fetch. Prologue ops
 // (quantize, embedding) run before the first GEMV.
 template <bool kFull>
-__device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint32_t* rd_cnt, int iol, int wg, int G,
+__device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint32_t* prog, int iol, int wg, int G,
                                          uint32_t base_tag) {
   for (int i = 0; i < nops; ++i) {
     const OpDev& op = L.opd[i];
@@ -1380,7 +1401,7 @@ __device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint
     EarlyFetch ef;
     bool early_done = !early;
     if (early) early_issue(L.opd[nx], iol, base_tag, ef);
-    wait_readers(sgpr(op.war_op), rd_cnt, G, L, ctl);
+    wait_readers(sgpr(op.war_op), prog, G, L, ctl, base_tag, iol & 63);
     // Finish the early fetch now if its input is all published (usual: its
     // producers are two or more ops back), while this op's first units are
     // still being computed. Waiting for these loads later would also wait
@@ -1389,8 +1410,9 @@ __device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint
     io_publish<kFull>(op, L, wg, G, iol, base_tag, ctl);
     lds_barrier();  // B: every compute wave is done with the op's input
     const bool io0 = sgpr(iol >> 6) == 0;  // the first I/O wave
-    if (sgpr(op.count_reads) && io0 && first_lane(iol))
-      (void)__hip_atomic_fetch_add(rd_cnt + i, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (sgpr(op.count_reads) && io0 && first_lane(iol))  // this workgroup has fetched op i's input
+      __hip_atomic_store((__attribute__((address_space(1))) uint32_t*)(prog + wg), base_tag + (uint32_t)i + 1,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (kFull && sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
       const uint64_t k = key_max(L.argk[0], L.argk[1]);
       uint64_t* dst = sgpr_ptr(as_const(sgpr_ptr(L.head))->parts) + 2 * wg;
@@ -1410,7 +1432,7 @@ __device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint
 // without that code.
 template <bool kFull>
 __global__ void __launch_bounds__(threads_of<kFull>()) step_kernel(const OpDev* __restrict__ ops, int nops, int first_gemv,
-                                                        Ctl* ctl, uint32_t* rd_cnt, const PrepDev* __restrict__ preps,
+                                                        Ctl* ctl, uint32_t* prog, const PrepDev* __restrict__ preps,
                                                         const HeadDev* __restrict__ head) {
   constexpr int kCW = cw_of<kFull>(), kThreads = threads_of<kFull>();
   __shared__ Lds<kFull> L;
@@ -1450,7 +1472,7 @@ __global__ void __launch_bounds__(threads_of<kFull>()) step_kernel(const OpDev* 
     // (at the compute waves' priority: raised above them, the I/O waves'
     // polls took issue slots from the preps of whole-token programs, 3.41
     // against 3.23 ms per token, and gained nothing for a plain chain)
-    io_waves<kFull>(L, nops, ctl, rd_cnt, threadIdx.x - 64 * kCW, wg, G, base_tag);
+    io_waves<kFull>(L, nops, ctl, prog, threadIdx.x - 64 * kCW, wg, G, base_tag);
   }
 
   // ---------------- end of step: count the workgroup out; the last one to
@@ -1480,7 +1502,7 @@ struct StepProgram {
   int first = 0;  // index of the first GEMV op
   OpDev* d_ops = nullptr;
   Ctl* d_ctl = nullptr;
-  uint32_t* d_cnt = nullptr;    // per-op reader counters
+  uint32_t* d_cnt = nullptr;    // per-workgroup progress words (write-after-read guards)
   PrepDev* d_preps = nullptr;   // the ops' prep descriptors
   HeadDev* d_head = nullptr;    // the greedy pick
   bool full = false;            // any prep, embedding or pick: the kFull kernel
@@ -1973,7 +1995,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   P->nops = (int)ops.size();
   if (!(P->d_ops = static_cast<OpDev*>(alloc(ops.size() * sizeof(OpDev)))) ||
       !(P->d_ctl = static_cast<Ctl*>(alloc(sizeof(Ctl)))) ||
-      !(P->d_cnt = static_cast<uint32_t*>(alloc(ops.size() * sizeof(uint32_t)))) ||
+      !(P->d_cnt = static_cast<uint32_t*>(alloc(256 * sizeof(uint32_t)))) ||
       !(P->d_preps = static_cast<PrepDev*>(alloc(preps.size() * sizeof(PrepDev)))) ||
       !(P->d_head = static_cast<HeadDev*>(alloc(sizeof(HeadDev)))))
     return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
