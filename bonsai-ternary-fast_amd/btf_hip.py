@@ -134,6 +134,7 @@ _step_launch = _decl("btf_hip_step_launch", [_vp, _vp])
 _step_error = _decl("btf_hip_step_error", [_vp, C.POINTER(C.c_int)])
 _step_destroy = _decl("btf_hip_step_destroy", [_vp])
 _step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
+_step_guards = _decl("btf_hip_step_guards", [_vp, C.POINTER(C.c_int)])
 _gguf_open = _decl("btf_hip_gguf_open", [C.c_char_p, _i, C.POINTER(C.c_void_p)])
 _gguf_close = _decl("btf_hip_gguf_close", [_vp])
 _gguf_info = _decl("btf_hip_gguf_info", [_vp, C.POINTER(_GgufHeader)])
@@ -161,7 +162,8 @@ ABI_SYMBOLS = (
     "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
     "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
     "btf_hip_graph_destroy", "btf_hip_step_create", "btf_hip_step_launch", "btf_hip_step_error",
-    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_step_create_ops", "btf_hip_gguf_open",
+    "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_step_guards", "btf_hip_step_create_ops",
+    "btf_hip_gguf_open",
     "btf_hip_gguf_close",
     "btf_hip_gguf_info", "btf_hip_gguf_tensor", "btf_hip_gguf_find_tensor", "btf_hip_gguf_kv",
     "btf_hip_gguf_find_kv", "btf_hip_gguf_kv_num", "btf_hip_gguf_kv_str", "btf_hip_ggml_row_bytes",
@@ -490,6 +492,12 @@ class StepProgram:
 
     def set_spin_limit(self, polls: int):
         _check(_step_spin(self.h, polls))
+
+    def guards(self) -> int:
+        """Ops that keep a write-after-read wait (test hook)."""
+        g = C.c_int()
+        _check(_step_guards(self.h, C.byref(g)))
+        return g.value
 
     def close(self, _destroy=_step_destroy):
         if getattr(self, "h", None):

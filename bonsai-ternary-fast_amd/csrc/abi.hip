@@ -358,6 +358,11 @@ int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls) {
   return step_set_spin_limit(static_cast<StepProgram*>(prog), polls);
 }
 
+int btf_hip_step_guards(btf_step_t prog, int* guards) {
+  if (!prog || !guards) return fail(BTF_ERR_ARGS, "step: null argument");
+  return step_guards(static_cast<StepProgram*>(prog), guards);
+}
+
 int btf_hip_step_destroy(btf_step_t prog) {
   step_destroy(static_cast<StepProgram*>(prog));
   return BTF_OK;

@@ -185,6 +185,7 @@ int step_check_residency(const DevState& ds);
 int step_launch(StepProgram* P, hipStream_t st);
 int step_error(StepProgram* P, int* err);
 int step_set_spin_limit(StepProgram* P, uint32_t polls);
+int step_guards(StepProgram* P, int* guards);
 void step_destroy(StepProgram* P);
 
 int gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst, hipStream_t st,

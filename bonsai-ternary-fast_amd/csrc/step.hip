@@ -1506,6 +1506,7 @@ struct StepProgram {
   PrepDev* d_preps = nullptr;   // the ops' prep descriptors
   HeadDev* d_head = nullptr;    // the greedy pick
   bool full = false;            // any prep, embedding or pick: the kFull kernel
+  int guards = 0;               // ops that keep a write-after-read wait (not implied by the data flow)
   std::vector<void*> bufs;      // every device buffer the program owns
 };
 
@@ -1751,6 +1752,14 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   // producer X, each of which had passed B of the GEMV before X. Workgroup v
   // has passed B of every earlier op before starting an op.
   std::vector<int> known((size_t)G * G, -1);
+  // allk[v]: the last GEMV whose barrier B every workgroup has surely
+  // passed, as far as workgroup v can tell; ax[op]: what every writer of op
+  // knew of all workgroups when it published (the minimum over them), which
+  // a reader of op's output learns too (its writers published after
+  // knowing it). If every workgroup writes units of an op, its readers know
+  // that all had passed B of the GEMV before it.
+  std::vector<int> allk(G, -1);
+  std::vector<int> ax;  // per device op
   int last_gemv = -1;                   // device index of the previous GEMV
   std::vector<int> prev_gemv;           // per device op: the GEMV before it (-1: none)
   auto owns = [&](const OpDev& x, int w) { return (w - x.rot + G) % G < x.units; };
@@ -1804,6 +1813,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     place(o, 1.0, -1);
     prologue_of[v] = (int)ops.size();
     ops.push_back(o);
+    ax.push_back(-1);
     prev_gemv.push_back(-1);
   }
   for (int i = 0; i < nuops; ++i) {
@@ -1828,6 +1838,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     place(o, 1.0, -1);
     dev_of[i] = (int)ops.size();
     ops.push_back(o);
+    ax.push_back(-1);
     prev_gemv.push_back(-1);
   }
   auto dev_writer = [&](int v, int k) {
@@ -1906,10 +1917,30 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
       for (int r : v0.old_readers) last = std::max(last, r);
       if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
     }
+    // What this op's writers learn from its input: they read all of it
+    // before publishing any unit (a unit spans every slice), so it counts for
+    // this op's own guard.
+    {
+      const int x = (int)o.in_tag - 1;  // input producer
+      const int px = x < (int)prev_gemv.size() ? prev_gemv[x] : -1;
+      if (ops[x].kind == 1) {
+        int a_in = ax[x];
+        bool all_write = px >= 0;
+        for (int w = 0; w < G && all_write; ++w) all_write = owns(ops[x], w);
+        if (all_write) a_in = std::max(a_in, px);
+        for (int v = 0; v < G; ++v) {
+          if (!owns(o, v)) continue;
+          allk[v] = std::max(allk[v], a_in);
+          if (px >= 0)
+            for (int w = 0; w < G; ++w)
+              if (owns(ops[x], w)) known[(size_t)v * G + w] = std::max(known[(size_t)v * G + w], px);
+        }
+      }
+    }
     if (war >= 0) {  // implied for every workgroup that writes this op's output?
       bool implied = true;
       for (int v = 0; v < G && implied; ++v) {
-        if (!owns(o, v)) continue;
+        if (!owns(o, v) || allk[v] >= war) continue;
         for (int w = 0; w < G; ++w)
           if (w != v && known[(size_t)v * G + w] < war) {
             implied = false;
@@ -1919,14 +1950,10 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
       if (implied) war = -1;
     }
     {
-      const int x = (int)o.in_tag - 1;  // input producer
-      const int px = x < (int)prev_gemv.size() ? prev_gemv[x] : -1;
-      if (ops[x].kind == 1 && px >= 0)
-        for (int v = 0; v < G; ++v) {
-          if (!owns(o, v)) continue;
-          for (int w = 0; w < G; ++w)
-            if (owns(ops[x], w)) known[(size_t)v * G + w] = std::max(known[(size_t)v * G + w], px);
-        }
+      int axo = INT_MAX;
+      for (int v = 0; v < G; ++v)
+        if (owns(o, v)) axo = std::min(axo, allk[v]);
+      ax.push_back(axo == INT_MAX ? -1 : axo);
     }
     o.war_op = war;
     if (war >= 0) ops[war].count_reads = 1;
@@ -1993,6 +2020,7 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   P->full = pick != nullptr || std::any_of(ops.begin(), ops.end(), [](const OpDev& o) { return o.prep >= 0 || o.kind == 2; });
   if (preps.empty()) preps.push_back(PrepDev{});
   P->nops = (int)ops.size();
+  P->guards = (int)std::count_if(ops.begin(), ops.end(), [](const OpDev& o) { return o.war_op >= 0; });
   if (!(P->d_ops = static_cast<OpDev*>(alloc(ops.size() * sizeof(OpDev)))) ||
       !(P->d_ctl = static_cast<Ctl*>(alloc(sizeof(Ctl)))) ||
       !(P->d_cnt = static_cast<uint32_t*>(alloc(256 * sizeof(uint32_t)))) ||
@@ -2050,6 +2078,11 @@ int step_launch(StepProgram* P, hipStream_t st) {
                                  dim3(P->G), dim3(P->full ? threads_of<true>() : threads_of<false>()), args, 0, st);
   if (e != hipSuccess) return fail(BTF_ERR_LAUNCH, std::string("step kernel: ") + hipGetErrorString(e));
   return launch_status("step_kernel");
+}
+
+int step_guards(StepProgram* P, int* guards) {
+  *guards = P->guards;
+  return BTF_OK;
 }
 
 int step_error(StepProgram* P, int* err) {

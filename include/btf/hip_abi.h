@@ -225,6 +225,10 @@ int btf_hip_step_destroy(btf_step_t prog);
  * later launches (0 restores the default, about one second). A tiny bound
  * makes a launch give up waiting and set the error flag instead of hanging. */
 int btf_hip_step_set_spin_limit(btf_step_t prog, uint32_t polls);
+/* Test hook: the number of the program's ops that keep a write-after-read
+ * wait (an op overwriting a buffer version that a workgroup may still have to
+ * read, where the data flow does not already order every read before it). */
+int btf_hip_step_guards(btf_step_t prog, int* guards);
 
 /* A whole batch-1 decode step in one launch: the step program with the ops
  * either side of the GEMV chain and each GEMV's full input prep. It replaces

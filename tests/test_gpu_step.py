@@ -183,6 +183,9 @@ def test_step_reordered_chain_and_war(hip, oracle):
 
     vecs, t = vectors()
     prog = hip.StepProgram(vecs, ops)
+    # the final STORE into vector 5's user buffer keeps its wait for the read
+    # of that data: the data flow before it does not order every read
+    assert prog.guards() >= 1
     for rep in range(2):
         if rep:
             for x, a in zip(t, inputs):
