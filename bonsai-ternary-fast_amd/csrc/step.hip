@@ -983,6 +983,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
             ready &= __hip_atomic_load(&L.early_seq[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >=
                      (uint32_t)cur.i + 1;
           if (ready || !poll_step(spins, L, ctl)) break;
+          __builtin_amdgcn_s_sleep(2);  // (an LDS poll: paced)
         }
         asm volatile("" ::: "memory");
       } else {
@@ -997,6 +998,9 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
             while (__hip_atomic_load(&L.sready[ob][sl], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) !=
                    (uint32_t)cur.i + 1) {
               if (!poll_step(spins, L, ctl)) break;
+              // an LDS poll returns at once: paced, so that the waves preparing
+              // the slices on the same SIMD keep its issue slots
+              __builtin_amdgcn_s_sleep(2);
             }
           }
           asm volatile("" ::: "memory");
