@@ -1025,6 +1025,13 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
     // One batch: consume ring slot r, refill it with entry r of the batch at
     // `a` (loads through `ld` / `lo`), then the batch's row sums and count.
     auto run_batch = [&](int b, const OpLd& ld, const LaneOff& lo, const BAddr& a, const BPos& np, bool last) {
+      // With preps in the program, a wave still holding real items of the op
+      // issues ahead of the waves that only refill (their batches past the
+      // op's items) or prepare slices; the plain kernel measured slower with it.
+      if constexpr (kFull) {
+        if (b * kRing < cur.n) __builtin_amdgcn_s_setprio(1);
+        else __builtin_amdgcn_s_setprio(0);
+      }
       float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
@@ -1069,6 +1076,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       lo_cur = lane_off(ld_cur, l16, grp);
       run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nw.first, G, BPos{nw.u0, nw.s0, nw.q0}), cp, true);
     }
+    if constexpr (kFull) __builtin_amdgcn_s_setprio(0);
     lds_barrier();  // B: every wave is done with the op
     if (cur.next >= nops) break;
     opi = cur.next;
