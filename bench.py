@@ -171,6 +171,14 @@ class Step:
                              torch.zeros((M, Kmax // 32), dtype=torch.float32, device="cuda"),
                              torch.zeros((M, Kmax // 32), dtype=torch.int32, device="cuda"))
         self.with_output = with_output
+        # the batched chain with the quantizes in the producers' epilogues (layer_qchain):
+        # Q8 rows of the residual, the attention-output stand-in, x and h
+        self.qa = None
+        if 3 <= M <= 32:
+            q8 = lambda K: hip.Q8Act(torch.zeros((M, K), dtype=torch.int8, device="cuda"),
+                                     torch.zeros((M, K // 32), dtype=torch.float32, device="cuda"),
+                                     torch.zeros((M, K // 32), dtype=torch.int32, device="cuda"))
+            self.qa = {"res": q8(E), "xo": q8(E), "x": q8(E), "h": q8(F)}
         # algorithmic bytes
         b_gemv = {"qkv": gemv_bytes(QKV, E, M), "o": gemv_bytes(E, E, M), "gateup": gemv_bytes(F, E, M, 1, 2),
                   "down": gemv_bytes(E, F, M, 2), "output": gemv_bytes(V, E, 1)}
@@ -221,6 +229,25 @@ class Step:
                            mode=G.kSwiglu, stream=st)
         self.prep(self.h, F, M, st)
         self.gemv([S.seg("down", l, self.res, E)], F, M, G.kAdd, st)
+
+    def layer_qchain(self, l, st):
+        """The layer of `layer` for a batch (3..32 rows) with the quantizes in
+        the producers' epilogues (btf_hip_launch_gemv_ex with a Q8 output,
+        one int8-MFMA launch each): o, gate+up and down write the Q8 rows of
+        x, h and the residual for the GEMM after them; the attention-output
+        stand-in keeps its own quantize launch. 5 launches instead of 8."""
+        S, M, G, hip, qa = self.S, self.M, self.S.hip.GemvMode, self.S.hip, self.qa
+        hip.launch_prep(self.xo, E, M, E, None, 0.0, None, None, 0, qa["xo"], st)
+        hip.launch_gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, qa["res"], G.kStore, st)
+        hip.launch_gemv_ex([S.seg("o", l, self.x, E)], E, M, a=qa["xo"], mode=G.kStore, out=qa["x"], stream=st)
+        hip.launch_gemv_ex([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, a=qa["x"],
+                           mode=G.kSwiglu, out=qa["h"], stream=st)
+        hip.launch_gemv_ex([S.seg("down", l, self.res, E)], F, M, a=qa["h"], mode=G.kAdd, out=qa["res"], stream=st)
+
+    def run_qchain(self, st):
+        self.S.hip.launch_prep(self.res, E, self.M, E, None, 0.0, None, None, 0, self.qa["res"], st)
+        for l in range(self.layers):
+            self.layer_qchain(l, st)
 
     def run_chain(self, st):
         for l in range(self.layers):
@@ -303,6 +330,19 @@ class Step:
         """One GEMV launch of a given kind (for per-kernel timing); fused: the
         launch of the chain engine (quantizes fused in)."""
         S, M, G = self.S, self.M, self.S.hip.GemvMode
+        if fused and M > 1:  # as in run_qchain
+            qa, hip = self.qa, S.hip
+            if kind == "qkv":
+                hip.launch_gemv([S.seg("qkv", l, self.qkv, QKV)], E, M, qa["res"], G.kStore, st)
+            elif kind == "o":
+                hip.launch_gemv_ex([S.seg("o", l, self.x, E)], E, M, a=qa["xo"], mode=G.kStore, out=qa["x"], stream=st)
+            elif kind == "gateup":
+                hip.launch_gemv_ex([S.seg("gate", l, self.h, F), S.seg("up", l, None, 0)], E, M, a=qa["x"],
+                                   mode=G.kSwiglu, out=qa["h"], stream=st)
+            else:
+                hip.launch_gemv_ex([S.seg("down", l, self.res, E)], F, M, a=qa["h"], mode=G.kAdd, out=qa["res"],
+                                   stream=st)
+            return
         if fused and kind in ("qkv", "o", "gateup"):  # as in run_chain
             x, segs, mode = {
                 "qkv": (self.res, [S.seg("qkv", l, self.qkv, QKV)], G.kStore),
@@ -538,19 +578,42 @@ def gemm_roofline(step, per, traffic_tab=None, workload="batched"):
 
 def run_batched_sub(S: Setup, M, layers, steps, warmup, traffic_tab):
     """Batched decode (M <= 32) or prefill (M = 512) on the first `layers`
-    layers of the sweep's weights: the graph of quantize + GEMM launches, and
-    the dominant kind's roofline."""
+    layers of the sweep's weights: the graph of quantize + GEMM launches and,
+    for 3 <= M <= 32, the graph with the quantizes in the producers'
+    epilogues (checked bit-exact against it); the faster one's dominant kind
+    and its roofline."""
     step = Step(S, M, layers, with_output=False)
     hip, torch = S.hip, S.torch
-    ms = time_graph(hip, torch, step.run, steps, warmup)
-    per = kind_timings(step, layers, steps)
-    dom, roof = gemm_roofline(step, per, traffic_tab)
-    log(f"M={M}: {ms:.4f} ms per {layers}-layer step; dominant {dom} {per[dom]['avg_us']} us, "
+    runs = {"graph": step.run}
+    verified = None
+    if step.qa is not None:
+        ok, why = verify_vs_graph(torch, step, step.run_qchain)
+        if not ok:
+            raise SystemExit(f"M={M}: fused-quantize launches do not match the op-by-op launches: {why}")
+        verified = why
+        runs["fused"] = step.run_qchain
+    ems = {}
+    for name, fn in runs.items():
+        step.reset()
+        ems[name] = time_graph(hip, torch, fn, steps, warmup)
+    best = min(ems, key=ems.get)
+    ms = ems[best]
+    per = kind_timings(step, layers, steps, fused=best == "fused")
+    dom, roof = gemm_roofline(step, per, traffic_tab if best == "graph" else None)
+    log(f"M={M}: {ms:.4f} ms per {layers}-layer step ({best}; " +
+        ", ".join(f"{k} {v:.4f}" for k, v in ems.items()) + f"); dominant {dom} {per[dom]['avg_us']} us, "
         f"{roof['achieved']} {roof['unit']} ({100 * roof['frac']:.1f} %)")
-    return {"workload": (f"batched decode, M={M}, " if M <= 32 else f"prefill, M={M}, ") +
-                        f"{layers} layers of the 27B shapes, graph of quantize + GEMM launches",
-            "batch": M, "ms_per_step": round(ms, 4), "bytes_per_step": step.total_bytes,
-            "GBs": round(step.total_bytes / (ms * 1e-3) / 1e9, 1), "kinds": per, "roofline": roof}
+    how = {"graph": "graph of quantize + GEMM launches",
+           "fused": "graph of GEMM launches quantizing their outputs in the epilogue (+ the attention-output "
+                    "stand-in's quantize)"}[best]
+    out = {"workload": (f"batched decode, M={M}, " if M <= 32 else f"prefill, M={M}, ") +
+                       f"{layers} layers of the 27B shapes, {how}",
+           "batch": M, "ms_per_step": round(ms, 4), "bytes_per_step": step.total_bytes,
+           "GBs": round(step.total_bytes / (ms * 1e-3) / 1e9, 1), "engines_ms": {k: round(v, 4) for k, v in ems.items()},
+           "kinds": per, "roofline": roof}
+    if verified:
+        out["verified"] = f"fused vs graph: {verified}"
+    return out
 
 
 def time_graph(hip, torch, fn, reps, warmup):
@@ -975,9 +1038,13 @@ def main():
     else:
         step = Step(S, 512, layers, with_output=False)
 
-    engines = [args.engine] if args.engine != "auto" else (["step", "chain", "graph"] if step.M == 1 else ["graph"])
-    if ("step" in engines or "chain" in engines) and step.M != 1:
-        raise SystemExit("the step and chain engines run batch-1 chains only")
+    engines = [args.engine] if args.engine != "auto" else (
+        ["step", "chain", "graph"] if step.M == 1 else ["chain", "graph"] if step.qa is not None else ["graph"])
+    if "step" in engines and step.M != 1:
+        raise SystemExit("the step engine runs batch-1 chains only")
+    if "chain" in engines and step.M != 1 and step.qa is None:
+        raise SystemExit("the chain engine runs batch 1 or 3..32 rows")
+    chain_fn = step.run_chain if step.M == 1 else step.run_qchain
 
     verified = {}
     engine_ms = {}
@@ -999,13 +1066,13 @@ def main():
             prog.close()
         log(f"step engine: {engine_ms['step']:.4f} ms per step")
     if "chain" in engines:
-        ok, why = verify_vs_graph(torch, step, lambda st: step.run_chain(st))
+        ok, why = verify_vs_graph(torch, step, chain_fn)
         verified["chain"] = why
         log(f"chain launches vs op-by-op launches: {why}")
         if not ok:
             raise SystemExit(f"chain launches do not match the op-by-op launches: {why}")
         step.reset()
-        engine_ms["chain"] = time_graph(hip, torch, step.run_chain, args.steps, args.warmup)
+        engine_ms["chain"] = time_graph(hip, torch, chain_fn, args.steps, args.warmup)
         log(f"chain engine: {engine_ms['chain']:.4f} ms per step")
     if "graph" in engines:
         step.reset()
@@ -1037,7 +1104,7 @@ def main():
             log(f"  PTQ1_0-direct {kind}: {avg_us:.3f} us/launch, {b3['kinds'][kind]['GBs']} GB/s")
     engine = min(engine_ms, key=engine_ms.get)
     ms = engine_ms[engine]
-    kernels_per_step = {"step": 1, "chain": layers * 5 + (2 if step.with_output else 0)}.get(
+    kernels_per_step = {"step": 1, "chain": layers * 5 + (2 if step.with_output else 1)}.get(
         engine, layers * 8 + (2 if step.with_output else 0))
     log(f"{engine} engine reported: {ms:.4f} ms per step ({step.total_bytes / 1e9:.4f} GB algorithmic)")
     value = step.total_bytes / (ms / 1e3) / 1e9
@@ -1103,7 +1170,7 @@ def main():
                 "kernel": f"{dom} GEMV (gemv_dot4_kernel{', quantizes fused in' if fk else ''})",
                 "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
     else:
-        _, roof = gemm_roofline(step, per, traffic_tab if not args.mfma_min_m else {})
+        _, roof = gemm_roofline(step, per, traffic_tab if not args.mfma_min_m and engine == "graph" else {})
 
     # Sub-results of the default run, each with its own roofline: the whole
     # decode step in one launch; config 1 (the 5120 -> 5120 GEMV, 64 distinct

@@ -254,6 +254,9 @@ int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, con
   for (int i = 0; i < nseg; ++i) sg[i] = {segs[i].codes, segs[i].scales, segs[i].N, segs[i].y, segs[i].ldy};
   const Q8 in = a ? Q8{a->q, a->d, a->s} : Q8{nullptr, nullptr, nullptr};
   const Q8 qo = out ? Q8{out->q, out->d, out->s} : Q8{nullptr, nullptr, nullptr};
+  // Q8 rows in, Q8 rows out, a batch on the int8-MFMA path: one launch (32-row output tiles)
+  if (a && out && M >= g_mfma_min_m && M <= 32)
+    return gemm_mfma(sg, nseg, K, 0, M, in, mode, nullptr, static_cast<hipStream_t>(stream), *ds, &qo);
   for (int m = 0; m < M; ++m) {
     rc = gemv_dot4(sg, nseg, K, m, 1, in, mode, nullptr, static_cast<hipStream_t>(stream), *ds, x, ldx,
                    out ? &qo : nullptr);

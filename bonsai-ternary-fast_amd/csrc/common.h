@@ -165,8 +165,9 @@ int gemv_dot4(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a,
 // PTQ1_0 path (codes = PTQ1_0 rows, scales unused): rows m0 .. m0+nb-1 (nb <= 2), K <= 32768.
 int gemv_b3(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a, int mode, hipStream_t st,
             const DevState& ds);
+// qout: also the Q8 of the output rows (nb <= 32, N % 32 == 0), for the next GEMM.
 int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& a, int mode, int32_t* dump,
-              hipStream_t st, const DevState& ds);
+              hipStream_t st, const DevState& ds, const Q8* qout = nullptr);
 int mfma_rows_per_pass();
 
 int repack(const uint8_t* src, int64_t nblocks, uint8_t* codes, uint16_t* scales, hipStream_t st,

@@ -57,6 +57,11 @@ struct MfmaArgs {
   const int32_t* s;
   int m0, nb;
   int32_t* dump;
+  // optional Q8 of the outputs (segment 0 after the mode), for the next GEMM:
+  // q [.][N], d and s [.][N / 32] at activation row m0 + m (gemm_ks_kernel, TR = 2)
+  int8_t* oq;
+  float* od;
+  int32_t* os;
 };
 
 // KB 128-column blocks are staged per iteration (one round of loads per KB
@@ -306,11 +311,16 @@ __global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
 // chain per wave; the activation is re-read from L2 by each tile. Per wave
 // the row sums follow the 64-row kernel's order over its blocks, and the NW
 // wave partials are added in wave order: ((p0 + p1) + p2) + ...
-template <int NW, int MT, int KB, int MODE, bool DUMP>
+// TR = 2: the workgroup owns 32 weight rows (two 16-row tiles, each with its
+// gate and up rows), one Q8 block of the output for every activation row, so
+// it also writes the Q8 of its outputs (a.oq) with the q8 kernel's
+// arithmetic. The per-output sums do not depend on TR.
+template <int NW, int MT, int KB, int MODE, bool DUMP, int TR = 1>
 __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   constexpr int BM = 16 * MT;
-  constexpr int G = MODE == BTF_GEMV_SWIGLU ? 2 : 1;  // 16-row groups: gate (and up)
-  constexpr int RW = 16 * G;                          // staged rows per wave
+  constexpr int G1 = MODE == BTF_GEMV_SWIGLU ? 2 : 1;  // 16-row groups of a tile: gate (and up)
+  constexpr int G = G1 * TR;                           // 16-row groups: tile t, matrix g1 at t * G1 + g1
+  constexpr int RW = 16 * G;                           // staged rows per wave
   constexpr int CS = 8 * KB + 1;
   constexpr int QS = 32 * KB + 2;
   constexpr int NCV = (RW * 2 * KB + 63) / 64;  // per-lane 16-byte code loads
@@ -319,7 +329,8 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   constexpr int NDV = (BM * 4 * KB + 63) / 64;  // d / s loads
   __shared__ uint32_t cs[NW][RW * CS];
   __shared__ uint16_t scs[NW][RW * KB];
-  __shared__ uint32_t qsm[NW][BM * QS];
+  constexpr int QSM = BM * QS > G * 16 * BM ? BM * QS : G * 16 * BM;  // (also holds the partials)
+  __shared__ uint32_t qsm[NW][QSM];
   __shared__ float dsm[NW][4 * KB][BM];
   static_assert(sizeof(qsm) >= NW * G * 16 * BM * sizeof(float), "partials alias the q stage");
 
@@ -339,7 +350,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
   const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
   const int K = a.K;
   const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
-  const int n0 = (bx - tile0) * 16;
+  const int n0 = (bx - tile0) * 16 * TR;
   const int mb = blockIdx.y * BM;
 
   // this wave's blocks [kw0, kw1); every wave runs niter iterations so the
@@ -367,9 +378,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
       const int r = i / (2 * KB), part = i - r * (2 * KB);
       rc[j] = u32x4{0u, 0u, 0u, 0u};
       if (i < RW * 2 * KB && part < 2 * nkb) {
-        const int nr = n0 + (r & 15);
+        const int nr = n0 + 16 * ((r >> 4) / G1) + (r & 15);
         const int nc = nr < N ? nr : N - 1;
-        const uint8_t* cb = r >= 16 ? a.up_codes : codes;
+        const uint8_t* cb = (r >> 4) % G1 ? a.up_codes : codes;
         rc[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
       }
     }
@@ -379,9 +390,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
       const int r = i / KB, jj = i - r * KB;
       rsc[j] = 0;
       if (i < RW * KB && jj < nkb) {
-        const int nr = n0 + (r & 15);
+        const int nr = n0 + 16 * ((r >> 4) / G1) + (r & 15);
         const int nc = nr < N ? nr : N - 1;
-        const uint16_t* sb = r >= 16 ? a.up_scales : scales;
+        const uint16_t* sb = (r >> 4) % G1 ? a.up_scales : scales;
         rsc[j] = sb[(size_t)nc * nsc + kb0 + jj];
       }
     }
@@ -469,11 +480,11 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
           for (int g = 0; g < G; ++g) {
             const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[g], cin, 0, 0, 0);
             if constexpr (DUMP) {
-              const int n = n0 + li;
+              const int n = n0 + 16 * (g / G1) + li;
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int m = mb + 16 * mt + 4 * t + r;
-                if (g == 0 && m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + kb * 4 + sb] = I[r];
+                if (g % G1 == 0 && m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + kb * 4 + sb] = I[r];
               }
             } else {
 #pragma unroll
@@ -509,45 +520,72 @@ __global__ void __launch_bounds__(64 * NW) gemm_ks_kernel(MfmaArgs a) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[((w * G + g) * 16 + li) * BM + 16 * mt + 4 * t + r] = acc[g][mt][r];
   __syncthreads();
-  for (int idx = tid; idx < 16 * BM; idx += 64 * NW) {
-    const int rr = idx & 15, mm = idx >> 4;
+  // thread idx: output row rr = idx % RT of the tile, activation row mm = idx / RT
+  // (with TR = 2 a half-wave holds the 32 outputs of one activation row: one Q8 block)
+  constexpr int RT = 16 * TR;
+  for (int idx = tid; idx < RT * BM; idx += 64 * NW) {
+    const int rr = idx & (RT - 1), mm = idx / RT;
     const int n = n0 + rr, m = mb + mm;
-    if (m >= a.nb || n >= N) continue;
-    float v[G];
+    const bool live = m < a.nb && n < N;
+    if (TR == 1 && !live) continue;
+    const int gb = (rr >> 4) * G1;  // first group of the row's tile
+    float v[G1];
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float sacc = red[((0 * G + g) * 16 + rr) * BM + mm];
+    for (int g = 0; g < G1; ++g) {
+      float sacc = red[((0 * G + gb + g) * 16 + (rr & 15)) * BM + mm];
 #pragma unroll
-      for (int ww = 1; ww < NW; ++ww) sacc = sacc + red[((ww * G + g) * 16 + rr) * BM + mm];
+      for (int ww = 1; ww < NW; ++ww) sacc = sacc + red[((ww * G + gb + g) * 16 + (rr & 15)) * BM + mm];
       v[g] = sacc;
     }
     float* o = &y[(size_t)(a.m0 + m) * ldy + n];
-    if constexpr (MODE == BTF_GEMV_SWIGLU)
-      *o = v[0] / (1.0f + expf(-v[0])) * v[G - 1];
-    else if constexpr (MODE == BTF_GEMV_ADD)
-      *o += v[0];
-    else
-      *o = v[0];
+    float out = 0.f;
+    if (live) {
+      if constexpr (MODE == BTF_GEMV_SWIGLU)
+        out = v[0] / (1.0f + expf(-v[0])) * v[G1 - 1];
+      else if constexpr (MODE == BTF_GEMV_ADD)
+        out = *o + v[0];
+      else
+        out = v[0];
+      *o = out;
+    }
+    if constexpr (TR == 2) {
+      if (a.oq) {  // (uniform) the Q8 block of rows n0 .. n0 + 31 of activation row m
+        float dq;
+        int sq;
+        const int q = q8_half(out, dq, sq);
+        uint32_t wq = (uint32_t)(q & 0xff) << (8 * (rr & 3));
+        wq |= (uint32_t)dpp_i<0xB1>((int)wq);  // quad_perm(1,0,3,2)
+        wq |= (uint32_t)dpp_i<0x4E>((int)wq);  // quad_perm(2,3,0,1)
+        if (live) {
+          const size_t mr = (size_t)(a.m0 + m);
+          if ((rr & 3) == 0) *reinterpret_cast<uint32_t*>(a.oq + mr * N + n) = wq;
+          if (rr == 0) {
+            a.od[mr * (N / 32) + n0 / 32] = dq;
+            a.os[mr * (N / 32) + n0 / 32] = sq;
+          }
+        }
+      }
+    }
   }
 }
 
-template <int NW, int MT, bool DUMP>
+template <int NW, int MT, bool DUMP, int TR>
 void by_mode_ks(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int KB = MT >= 2 ? 1 : 2;  // small stages: occupancy (4-5 waves per SIMD) beats bytes per round
   if (mode == BTF_GEMV_STORE)
-    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_STORE, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
   else if (mode == BTF_GEMV_ADD)
-    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_ADD, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
   else
-    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((gemm_ks_kernel<NW, MT, KB, BTF_GEMV_SWIGLU, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
 }
 
-template <int MT, bool DUMP>
+template <int MT, bool DUMP, int TR = 1>
 void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   if (nw == 8)
-    by_mode_ks<8, MT, DUMP>(mode, a, grid, st);
+    by_mode_ks<8, MT, DUMP, TR>(mode, a, grid, st);
   else
-    by_mode_ks<4, MT, DUMP>(mode, a, grid, st);
+    by_mode_ks<4, MT, DUMP, TR>(mode, a, grid, st);
 }
 
 // Prefill tile (more than 32 activation rows): a workgroup owns 64 staged
@@ -1033,11 +1071,13 @@ void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
 int mfma_rows_per_pass() { return 64; }
 
 int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& act, int mode, int32_t* dump,
-              hipStream_t st, const DevState& ds) {
+              hipStream_t st, const DevState& ds, const Q8* qout) {
   MfmaArgs a{};
-  // up to 32 activation rows: the K-split 16-row tile; more: the 64-row tile
+  // up to 32 activation rows: the K-split 16-row tile (32 rows with a Q8
+  // output); more: the 64-row tile
   const bool ks = nb <= 32;
-  const int rows_real = ks ? 16 : mode == BTF_GEMV_SWIGLU ? 32 : 64;
+  if (qout && (!ks || dump)) return fail(BTF_ERR_ARGS, "gemm: a Q8 output needs at most 32 rows");
+  const int rows_real = ks ? (qout ? 32 : 16) : mode == BTF_GEMV_SWIGLU ? 32 : 64;
   const int nuse = mode == BTF_GEMV_SWIGLU ? 1 : nseg;
   int tiles = 0;
   for (int i = 0; i < 3; ++i) {
@@ -1065,6 +1105,11 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   a.m0 = m0;
   a.nb = nb;
   a.dump = dump;
+  if (qout) {
+    a.oq = const_cast<int8_t*>(qout->q);  // (Q8 holds read-only views; this one is written)
+    a.od = const_cast<float*>(qout->d);
+    a.os = const_cast<int32_t*>(qout->s);
+  }
   if (tiles == 0) return BTF_OK;
   const int MT = nb <= 16 ? 1 : nb <= 32 ? 2 : 4;
   const int BM = 16 * MT;
@@ -1075,6 +1120,14 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
     // QKV 11.0 -> 10.1 us at M = 8), except gate+up at K = 5120 (27 -> 31 us);
     // with two activation tiles 8 waves were slower on every shape
     const int nw = MT == 1 && (K >= 8192 || mode != BTF_GEMV_SWIGLU) ? 8 : 4;
+    // (the K split depends on nw only: the outputs do not depend on the tile height)
+    if (qout) {
+      if (MT == 1)
+        by_waves_ks<1, false, 2>(nw, mode, a, grid, st);
+      else
+        by_waves_ks<2, false, 2>(nw, mode, a, grid, st);
+      return launch_status("gemm_ks_kernel");
+    }
     if (MT == 1)
       dmp ? by_waves_ks<1, true>(nw, mode, a, grid, st) : by_waves_ks<1, false>(nw, mode, a, grid, st);
     else

@@ -145,7 +145,9 @@ int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q
                           btf_stream_t stream);
 
 /* launch_gemv with the Q8_0 quantizes of a GEMV chain fused in (the v_dot4
- * kernel, one launch per activation row):
+ * kernel, one launch per activation row; with Q8 rows in, a Q8 output and a
+ * batch of 3..32 rows on the int8-MFMA path (btf_hip_gemv_set_policy), one
+ * launch of the MFMA kernel with 32-row output tiles):
  *  - input: exactly one of `a` (Q8 rows, as launch_gemv) or `x` (fp32 rows
  *    [M][ldx], quantized inside the launch with launch_prep's arithmetic, no
  *    norm or transform; x 16-byte aligned, ldx >= K, ldx % 4 == 0);
@@ -154,7 +156,8 @@ int btf_hip_gemv_i32_dump(const uint8_t* codes, int N, int K, int M, const btf_q
  *    GEMV (q [M][N], d and s [M][N/32]); one output segment, N % 32 == 0,
  *    K <= 20480 (swiglu K <= 10240).
  * The results (y, and the Q8 rows) are bit-identical to launch_prep +
- * launch_gemv on the v_dot4 path. No reference counterpart: the reference
+ * launch_gemv on the same path (v_dot4 or MFMA) followed by launch_prep of
+ * the output. No reference counterpart: the reference
  * decoder launches the quantize and the GEMV separately
  * (src/cuda/gpu_decoder.cu:411-418). */
 int btf_hip_launch_gemv_ex(const btf_gemv_seg* segs, int nseg, int K, int M, const btf_q8act* a, const float* x,

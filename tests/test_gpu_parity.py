@@ -616,6 +616,79 @@ def test_gemv_fused_output_quantize(hip, oracle, K, N, M, xin):
         assert np.array_equal(host(out.s), rs), f"s, mode {mode}"
 
 
+@pytest.mark.parametrize("K,N,M", [(5120, 160, 3), (5120, 96, 8), (17408, 64, 8), (5120, 128, 16),
+                                   (1024, 96, 20), (17408, 64, 32)])
+def test_gemm_fused_output_quantize_batched(hip, oracle, K, N, M):
+    """launch_gemv_ex with Q8 rows in and out for a batch (the int8-MFMA
+    K-split kernel with 32-row output tiles, one launch): y equals
+    launch_gemv's bit for bit, the Q8 rows equal the oracle's quantize of that
+    y bit for bit, and y is within the bars of the oracle GEMV, in every mode;
+    rows 0..31 of the plain matrix are all trit 0 (an all-zero output block)."""
+    rng = np.random.default_rng(7 + K + N + M)
+    x = (rng.standard_normal((M, K)) * 2).astype(np.float32)
+    q, d, s = oracle.quantize_rows(x)
+    torch = _torch()
+    a = q8_dev(q, d, s, hip)
+    mat, gate, up = (random_mat(oracle, rng, N, K) for _ in range(3))
+    mat[0][:32] = 0x55
+    y0 = rng.standard_normal((M, N)).astype(np.float32)
+    y0[:, :32] = 0.0
+    for mode in (hip.GemvMode.kStore, hip.GemvMode.kAdd, hip.GemvMode.kSwiglu):
+        if mode == hip.GemvMode.kSwiglu:
+            mk = lambda y: [hip.GemvSeg(dev(gate[0]), dev(gate[1]), N, y, N),
+                            hip.GemvSeg(dev(up[0]), dev(up[1]), N, None, 0)]
+        else:
+            mk = lambda y: [hip.GemvSeg(dev(mat[0]), dev(mat[1]), N, y, N)]
+        y_ref = dev(y0.copy())
+        hip.launch_gemv(mk(y_ref), K, M, a, mode, stream())
+        y = dev(y0.copy())
+        out = hip.Q8Act(zeros((M, N), torch.int8), zeros((M, N // 32), torch.float32), zeros((M, N // 32), torch.int32))
+        hip.launch_gemv_ex(mk(y), K, M, a=a, mode=mode, out=out, stream=stream())
+        yh = host(y)
+        assert np.array_equal(yh.view(np.uint32), host(y_ref).view(np.uint32)), f"y, mode {mode}"
+        rq, rd, rs = oracle.quantize_rows(yh)
+        assert np.array_equal(host(out.q), rq), f"q, mode {mode}"
+        assert np.array_equal(host(out.d).view(np.uint32), rd.view(np.uint32)), f"d, mode {mode}"
+        assert np.array_equal(host(out.s), rs), f"s, mode {mode}"
+        if mode == hip.GemvMode.kSwiglu:
+            ref = oracle.swiglu(oracle.gemv(gate[0], gate[1], K, q, d, s), oracle.gemv(up[0], up[1], K, q, d, s))
+        else:
+            ref = oracle.gemv(mat[0], mat[1], K, q, d, s, y=y0.copy(), add=mode == hip.GemvMode.kAdd)
+        assert_close_1e3(yh, ref, f"fused batched mode {mode}")
+
+
+def test_gemm_fused_batched_chain_matches_prep_chain(hip, oracle):
+    """Batched decode (M = 8) through a 3-GEMM chain whose quantizes ride in
+    the producers' epilogues equals the chain of launch_prep + launch_gemv
+    pairs bit for bit, y and the Q8 rows handed on."""
+    rng = np.random.default_rng(515)
+    M, K0, K1, K2 = 8, 2048, 4096, 1024
+    m0, m1, m2 = random_mat(oracle, rng, K1, K0), random_mat(oracle, rng, K2, K1), random_mat(oracle, rng, 96, K2)
+    x = rng.standard_normal((M, K0)).astype(np.float32)
+    torch = _torch()
+
+    def q8(n):
+        return hip.Q8Act(zeros((M, n), torch.int8), zeros((M, n // 32), torch.float32), zeros((M, n // 32), torch.int32))
+    res = []
+    for fused in (False, True):
+        xd = dev(x)
+        y1, y2, y3 = zeros((M, K1), torch.float32), zeros((M, K2), torch.float32), zeros((M, 96), torch.float32)
+        a0, a1, a2 = q8(K0), q8(K1), q8(K2)
+        hip.launch_prep(xd, K0, M, K0, None, 0.0, None, None, 0, a0, stream())
+        if fused:
+            hip.launch_gemv_ex([hip.GemvSeg(dev(m0[0]), dev(m0[1]), K1, y1, K1)], K0, M, a=a0, out=a1, stream=stream())
+            hip.launch_gemv_ex([hip.GemvSeg(dev(m1[0]), dev(m1[1]), K2, y2, K2)], K1, M, a=a1, out=a2, stream=stream())
+        else:
+            hip.launch_gemv([hip.GemvSeg(dev(m0[0]), dev(m0[1]), K1, y1, K1)], K0, M, a0, hip.GemvMode.kStore, stream())
+            hip.launch_prep(y1, K1, M, K1, None, 0.0, None, None, 0, a1, stream())
+            hip.launch_gemv([hip.GemvSeg(dev(m1[0]), dev(m1[1]), K2, y2, K2)], K1, M, a1, hip.GemvMode.kStore, stream())
+            hip.launch_prep(y2, K2, M, K2, None, 0.0, None, None, 0, a2, stream())
+        hip.launch_gemv([hip.GemvSeg(dev(m2[0]), dev(m2[1]), 96, y3, 96)], K2, M, a2, hip.GemvMode.kStore, stream())
+        res.append([host(t) for t in (y1, y2, y3, a1.q, a1.d, a1.s, a2.q, a2.d, a2.s)])
+    for u, v in zip(*res):
+        assert np.array_equal(u.view(np.uint8), v.view(np.uint8))
+
+
 def test_gemv_fused_chain_matches_prep_chain(hip, oracle):
     """A 3-GEMV chain whose quantizes ride in the GEMV launches (fp32 input
     quantized by the first, Q8 outputs feeding the next) equals the chain of
