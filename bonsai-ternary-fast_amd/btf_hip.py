@@ -200,12 +200,14 @@ def _check(rc: int):
         raise RuntimeError(_last_error().decode() or f"btf_hip error {rc}")
 
 
-def _finalize(obj):
+def _finalize(obj, _is_finalizing=sys.is_finalizing):
     """Release a handle from __del__, except at interpreter shutdown: then the
     HIP runtime (and a profiler attached to it) may already be torn down, and
     the process exit releases the device memory anyway. Owners that need a
-    deterministic release call close() themselves."""
-    if sys.is_finalizing():
+    deterministic release call close() themselves. (The finalizers bind this
+    function, and it binds sys.is_finalizing, as default arguments: at
+    shutdown the module's globals may already be cleared.)"""
+    if _is_finalizing():
         return
     obj.close()
 
@@ -504,8 +506,8 @@ class StepProgram:
             _destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def step_create_ops_raw(vecs, ops) -> int:
@@ -569,8 +571,8 @@ class Graph:
             _destroy(self.exec)
             self.exec = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 class Event:
@@ -594,8 +596,8 @@ class Event:
             _destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 class MappedHostBuffer:
@@ -615,8 +617,8 @@ class MappedHostBuffer:
             _free(self.host)
             self.host = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 GGUF_STRING, GGUF_ARRAY, GGUF_F32, GGUF_F64 = 8, 9, 6, 12
@@ -732,8 +734,8 @@ class Gguf:
             _close(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def ggml_row_bytes(ggml_type: int, n: int) -> int:
@@ -778,8 +780,8 @@ class Loader:
             _destroy(self.h)
             self.h = None
 
-    def __del__(self):
-        _finalize(self)
+    def __del__(self, _fin=_finalize):
+        _fin(self)
 
 
 def loader_create_raw(staging_bytes: int) -> int:
