@@ -61,6 +61,11 @@ INT8_PEAK_TOPS = 5000.0
 E, F, QKV, V, LAYERS = 5120, 17408, 7168, 248320, 64
 
 
+def under_profiler() -> bool:
+    """Is this process running under rocprofv3 (its tool library preloaded)?"""
+    return bool(os.environ.get("ROCPROFILER_LIBRARY_CTOR")) or "rocprofiler" in os.environ.get("LD_PRELOAD", "")
+
+
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -82,6 +87,49 @@ def b3_bytes(N, K, M, out_rw=1, nmat=1):
 
 def prep_bytes(K, M):
     return M * (4 * K + K + K // 4)
+
+
+SWEEP_VECS = (E, QKV, E, E, F, V)  # the sweep program's vector slots (the logits only with the output)
+TOKEN_VECS = (E, QKV, E, F, V)     # the whole-token program's vector slots
+
+
+def sweep_ops(hip, w, layers, with_output=True):
+    """The sweep's step program (batch 1), in the op-by-op order: every op
+    waits for the one before it, except o, whose input stands in for the
+    attention output. w(name, layer) -> (codes, scales) addresses. Vector
+    slots: 0 residual, 1 qkv, 2 attention-output stand-in, 3 x, 4 h, 5 logits."""
+    G = hip.GemvMode
+    ops = []
+    for l in range(layers):
+        gc, gs = w("gate", l)
+        uc, us = w("up", l)
+        ops.append(hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1))
+        ops.append(hip.StepGemv(G.kStore, E, E, *w("o", l), 2, 3))
+        ops.append(hip.StepGemv(G.kSwiglu, E, F, gc, gs, 3, 4, uc, us))
+        ops.append(hip.StepGemv(G.kAdd, F, E, *w("down", l), 4, 0))
+    if with_output:
+        ops.append(hip.StepGemv(G.kStore, E, V, *w("output", layers), 0, 5))
+    return ops
+
+
+def token_ops(hip, w, layers, tok, pos, hx, norms, signs, out_norm, out_signs, emb_signs):
+    """The whole-token step program: embedding, 64 x (QKV, o, gate+up, down)
+    each with its prep, the output projection and the greedy pick.
+    hx(signs) -> the transform (or None); norms[l] = (attention, FFN) RMSNorm
+    weights (or None); signs[l] = the qkv, o, gate/up and down inputs' signs.
+    Vector slots: 0 residual, 1 qkv, 2 attention-output stand-in, 3 h, 4 logits."""
+    G = hip.GemvMode
+    ops = [hip.StepEmbed(0, *w("embed", layers), tok, hx(emb_signs))]
+    for l in range(layers):
+        na, nf = norms[l]
+        sq, so_, sgu, sd = signs[l]
+        ops += [hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1, normw=na, eps=1e-6, hx=hx(sq)),
+                hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0, hx=hx(so_)),
+                hip.StepGemv(G.kSwiglu, E, F, *w("gate", l), 0, 3, *w("up", l), normw=nf, eps=1e-6, hx=hx(sgu)),
+                hip.StepGemv(G.kAdd, F, E, *w("down", l), 3, 0, hx=hx(sd))]
+    ops.append(hip.StepGemv(G.kStore, E, V, *w("output", layers), 0, 4, normw=out_norm, eps=1e-6, hx=hx(out_signs)))
+    ops.append(hip.StepArgmax(4, tok, pos))
+    return ops
 
 
 class Setup:
@@ -130,6 +178,12 @@ class Setup:
         self.weight_bytes = sum(N * K // 4 + N * K // 64 for (name, _), (N, K, _, _, _) in self.mats.items()
                                 if name != "embed")
         del stage
+
+    def weights(self, name, l):
+        """(codes, scales) device addresses of one matrix."""
+        N, K, mid, co, so = self.mats[(name, l)]
+        base = self.arena.data_ptr()
+        return base + co, base + so
 
     def seg(self, name, l, y, ldy):
         N, K, mid, co, so = self.mats[(name, l)]
@@ -306,25 +360,7 @@ class Step:
                 hip.StepVec(E, self.x), hip.StepVec(F, self.h)]
         if self.with_output:
             vecs.append(hip.StepVec(V, self.logits))
-        base = S.arena.data_ptr()
-
-        def w(name, l):
-            N, K, _, co, so = S.mats[(name, l)]
-            return base + co, base + so
-
-        # The op-by-op order; every op waits for the one before it, except o,
-        # whose input stands in for the attention output.
-        ops = []
-        for l in range(self.layers):
-            gc, gs = w("gate", l)
-            uc, us = w("up", l)
-            ops.append(hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1))
-            ops.append(hip.StepGemv(G.kStore, E, E, *w("o", l), 2, 3))
-            ops.append(hip.StepGemv(G.kSwiglu, E, F, gc, gs, 3, 4, uc, us))
-            ops.append(hip.StepGemv(G.kAdd, F, E, *w("down", l), 4, 0))
-        if self.with_output:
-            ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 5))
-        return hip.StepProgram(vecs, ops)
+        return hip.StepProgram(vecs, sweep_ops(hip, S.weights, self.layers, self.with_output))
 
     def kind_launch(self, kind, l, st, fused=False):
         """One GEMV launch of a given kind (for per-kernel timing); fused: the
@@ -425,26 +461,9 @@ class Token:
     def ops(self):
         """The step program's ops. Vector slots: 0 residual, 1 qkv, 2
         attention-output stand-in, 3 h, 4 logits."""
-        hip, S, G = self.S.hip, self.S, self.S.hip.GemvMode
-        base = S.arena.data_ptr()
-
-        def w(name, l):
-            N, K, _, co, so = S.mats[(name, l)]
-            return base + co, base + so
-
-        ops = [hip.StepEmbed(0, *w("embed", self.layers), self.tok, self.hx(self.emb_signs))]
-        for l in range(self.layers):
-            na, nf = self.norm[l]
-            sq, so_, sgu, sd = self.signs[l]
-            ops += [hip.StepGemv(G.kStore, E, QKV, *w("qkv", l), 0, 1, normw=self.nw(na), eps=1e-6, hx=self.hx(sq)),
-                    hip.StepGemv(G.kAdd, E, E, *w("o", l), 2, 0, hx=self.hx(so_)),
-                    hip.StepGemv(G.kSwiglu, E, F, *w("gate", l), 0, 3, *w("up", l), normw=self.nw(nf), eps=1e-6,
-                                 hx=self.hx(sgu)),
-                    hip.StepGemv(G.kAdd, F, E, *w("down", l), 3, 0, hx=self.hx(sd))]
-        ops.append(hip.StepGemv(G.kStore, E, V, *w("output", self.layers), 0, 4, normw=self.nw(self.out_norm),
-                                eps=1e-6, hx=self.hx(self.out_signs)))
-        ops.append(hip.StepArgmax(4, self.tok, self.pos))
-        return ops
+        return token_ops(self.S.hip, self.S.weights, self.layers, self.tok, self.pos, self.hx,
+                         [tuple(self.nw(w) for w in ln) for ln in self.norm], self.signs,
+                         self.nw(self.out_norm), self.out_signs, self.emb_signs)
 
     def vecs(self):
         hip = self.S.hip
@@ -971,6 +990,8 @@ def main():
     ap.add_argument("--no-b3", dest="b3", action="store_false")
     ap.add_argument("--mfma-min-m", type=int, default=0,
                     help="batch rows from which GEMVs run on the int8 MFMA kernels (0: the library default)")
+    ap.add_argument("--allow-profiler", action="store_true",
+                    help="launch step programs under rocprofv3 (see under_profiler)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="first run 3 device copies of 1 GiB (the scale reference for HBM counters)")
     args = ap.parse_args()
@@ -981,6 +1002,14 @@ def main():
                                    "is written up beside the code)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+
+    launches_step = args.workload == "token" or (args.workload == "sweep" and args.engine in ("auto", "step"))
+    if launches_step and under_profiler() and not args.allow_profiler:
+        raise SystemExit("bench: this run would launch step programs (a cooperative launch) under rocprofv3, "
+                         "whose teardown has ended every such run with a segmentation fault in the exit "
+                         "handlers after the results were complete; step timings come from HIP events on the "
+                         "kernel's stream. Pass --allow-profiler to run it anyway, or profile the other "
+                         "workloads (--workload layer|batched|prefill, --engine chain|graph).")
 
     import torch
     sys.path.insert(0, PKG)

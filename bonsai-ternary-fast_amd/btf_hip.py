@@ -60,6 +60,11 @@ class _StepOp(C.Structure):
                 ("d_tok_out", C.c_void_p), ("d_pos", C.c_void_p)]
 
 
+class _StepAudit(C.Structure):
+    _fields_ = [("stores", C.c_int64), ("outside", C.c_int64), ("ops", C.c_int), ("guards", C.c_int),
+                ("full", C.c_int), ("first_outside", C.c_char * 160)]
+
+
 class _DeviceInfo(C.Structure):
     _fields_ = [("cu_count", C.c_int), ("lds_bytes_per_block", C.c_int), ("max_clock_khz", C.c_int),
                 ("mem_clock_khz", C.c_int), ("mem_bus_width_bits", C.c_int), ("l2_bytes", C.c_int),
@@ -135,6 +140,8 @@ _step_error = _decl("btf_hip_step_error", [_vp, C.POINTER(C.c_int)])
 _step_destroy = _decl("btf_hip_step_destroy", [_vp])
 _step_spin = _decl("btf_hip_step_set_spin_limit", [_vp, C.c_uint32])
 _step_guards = _decl("btf_hip_step_guards", [_vp, C.POINTER(C.c_int)])
+_step_audit = _decl("btf_hip_step_audit",
+                    [C.POINTER(_StepVec), _i, C.POINTER(_StepOp), _i, _i, C.POINTER(_StepAudit)])
 _gguf_open = _decl("btf_hip_gguf_open", [C.c_char_p, _i, C.POINTER(C.c_void_p)])
 _gguf_close = _decl("btf_hip_gguf_close", [_vp])
 _gguf_info = _decl("btf_hip_gguf_info", [_vp, C.POINTER(_GgufHeader)])
@@ -163,6 +170,7 @@ ABI_SYMBOLS = (
     "btf_hip_event_elapsed_ms", "btf_hip_graph_begin", "btf_hip_graph_end", "btf_hip_graph_launch",
     "btf_hip_graph_destroy", "btf_hip_step_create", "btf_hip_step_launch", "btf_hip_step_error",
     "btf_hip_step_destroy", "btf_hip_step_set_spin_limit", "btf_hip_step_guards", "btf_hip_step_create_ops",
+    "btf_hip_step_audit",
     "btf_hip_gguf_open",
     "btf_hip_gguf_close",
     "btf_hip_gguf_info", "btf_hip_gguf_tensor", "btf_hip_gguf_find_tensor", "btf_hip_gguf_kv",
@@ -508,6 +516,18 @@ class StepProgram:
 
     def __del__(self, _fin=_finalize):
         _fin(self)
+
+
+def step_audit(vecs, ops, G: int = 256) -> dict:
+    """btf_hip_step_audit (host only, no device): the program for a grid of G
+    workgroups, every global store of a launch replayed and checked against
+    the buffers the program owns or was given. Pointers may be plain ints."""
+    cv = (_StepVec * len(vecs))(*[_StepVec(v.n, _addr(v.data)) for v in vecs])
+    co = (_StepOp * len(ops))(*[_step_op_c(o) for o in ops])
+    r = _StepAudit()
+    _check(_step_audit(cv, len(vecs), co, len(ops), G, C.byref(r)))
+    return {"stores": r.stores, "outside": r.outside, "ops": r.ops, "guards": r.guards, "full": bool(r.full),
+            "first_outside": r.first_outside.decode()}
 
 
 def step_create_ops_raw(vecs, ops) -> int:

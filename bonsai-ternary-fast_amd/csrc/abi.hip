@@ -346,6 +346,12 @@ int btf_hip_step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_o
   return rc;
 }
 
+int btf_hip_step_audit(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, int G,
+                       btf_step_audit* out) {
+  if (!vecs || !ops || !out || nvec <= 0 || nops <= 0) return fail(BTF_ERR_ARGS, "step: empty program");
+  return step_audit(vecs, nvec, ops, nops, G, out);
+}
+
 int btf_hip_step_launch(btf_step_t prog, btf_stream_t stream) {
   if (!prog) return fail(BTF_ERR_ARGS, "step: null program");
   return step_launch(static_cast<StepProgram*>(prog), static_cast<hipStream_t>(stream));

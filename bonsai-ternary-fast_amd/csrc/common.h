@@ -187,6 +187,7 @@ int step_launch(StepProgram* P, hipStream_t st);
 int step_error(StepProgram* P, int* err);
 int step_set_spin_limit(StepProgram* P, uint32_t polls);
 int step_guards(StepProgram* P, int* guards);
+int step_audit(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, int G, btf_step_audit* res);  // host only
 void step_destroy(StepProgram* P);
 
 int gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst, hipStream_t st,

@@ -6,25 +6,25 @@
 //   gemm_pf2_kernel  more rows (prefill): 64 weight rows x 64 or 128
 //                    activation rows, fed by an LDS-direct ring;
 //   gemm_pf_kernel   the same tile staged through registers (activation
-//                    scales not 16-byte aligned);
-//   gemm_mfma_kernel the first 64-row tile, kept for the exact-I dump of more
-//                    than 32 rows.
+//                    scales not 16-byte aligned).
+// Each has a DUMP instance (btf_hip_gemv_i32_dump) that writes the exact
+// int32 I of every (row, output, sub-block) from the same tile.
 //
-// The 64-row tile: a workgroup of 4 waves owns 64 weight rows (wave w: rows
-// 16w..16w+15; swiglu: waves 0-1 gate rows, waves 2-3 the matching up rows)
-// and BM = 16*MT activation rows. The K loop walks 128-column blocks (one
-// fp16 weight scale): codes (64 x 32 B), the block's scales, q (BM x 128 B)
-// and the activation d / -s (BM x 4) are staged in LDS, then every wave runs,
-// per 32-column sub-block,
-//     I = mfma_i32_16x16x32_i8(A = q, B = codes, C = -s)     (exact int32)
+// The prefill tile: a workgroup of 4 waves owns 64 weight rows (swiglu: 32
+// gate rows and the same 32 up rows) and BM = 32 * MW activation rows; the
+// K loop walks 128-column blocks (one fp16 weight scale): codes (64 x 32 B),
+// the block's scales, q (BM x 128 B) and the activation d (BM x 4) are staged
+// in LDS, then every wave runs, per 32-column sub-block,
+//     I = mfma_i32_16x16x32_i8(A = q, B = codes)              (exact int32)
 //     blk += d[m][s] * (float)I
 // and per block acc += fp16(scale[n]) * blk.
 // Lane l of a 16x16x32 MFMA holds A row (l%16) and B column (l%16) bytes for
 // k = 8*(l/16) .. +7; the codes for columns 8t..8t+7 of a sub-block are the
 // 2-bit fields {2(t%2), 2(t%2)+1} of its word t/2, so each lane unpacks its
 // B fragment with two shift+mask ops. C row 4*(l/16)+r, column l%16 lands in
-// accumulator r of lane l. The other kernels map the codes 0 / 1 / 2 to int8
-// -1 / 0 / +1 (one byte permute per word) and start the accumulator at 0.
+// accumulator r of lane l. gemm_pf_kernel starts the accumulator at -s (the
+// codes 0 / 1 / 2 as they are); gemm_pf2_kernel and gemm_ks_kernel map the
+// codes to int8 -1 / 0 / +1 (one byte permute per word) and start it at 0.
 #include <climits>
 
 #include "../../include/btf/hip_abi.h"
@@ -64,253 +64,15 @@ struct MfmaArgs {
   int32_t* os;
 };
 
-// KB 128-column blocks are staged per iteration (one round of loads per KB
-// blocks instead of per block: the loop is bound by load latency, not by
-// the MFMA work of a block).
-template <int MT, int KB, int MODE, bool DUMP>
-__global__ void __launch_bounds__(256) gemm_mfma_kernel(MfmaArgs a) {
-  constexpr int BM = 16 * MT;
-  constexpr int CS = 8 * KB + 1;   // words per staged code row (KB x 32 B + 4 B pad)
-  constexpr int QS = 32 * KB + 2;  // words per staged q row (KB x 128 B + 8 B pad)
-  __shared__ uint32_t cs[64 * CS];
-  __shared__ uint16_t scs[64 * KB];
-  __shared__ uint32_t qsm[BM * QS];
-  __shared__ float dsm[4 * KB][BM];
-  __shared__ int32_t nsm[4 * KB][BM];
-  __shared__ float upx[(MODE == BTF_GEMV_SWIGLU) ? 32 * BM : 1];
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int li = lane & 15;
-  const int t = lane >> 4;
-
-  const int bx = blockIdx.x;
-  const int seg = (bx >= a.tile_start[1]) + (bx >= a.tile_start[2]);
-  const uint8_t* codes = seg == 0 ? a.codes[0] : seg == 1 ? a.codes[1] : a.codes[2];
-  const uint16_t* scales = seg == 0 ? a.scales[0] : seg == 1 ? a.scales[1] : a.scales[2];
-  float* y = seg == 0 ? a.y[0] : seg == 1 ? a.y[1] : a.y[2];
-  const int N = seg == 0 ? a.N[0] : seg == 1 ? a.N[1] : a.N[2];
-  const int ldy = seg == 0 ? a.ldy[0] : seg == 1 ? a.ldy[1] : a.ldy[2];
-  const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
-  const int K = a.K;
-  const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
-
-  // staged row r (0..63) -> matrix row and source
-  constexpr int ROWS_REAL = MODE == BTF_GEMV_SWIGLU ? 32 : 64;
-  const int n0 = (bx - tile0) * ROWS_REAL;
-  const int mb = blockIdx.y * BM;  // first activation row of the tile (relative to m0)
-
-  float acc[MT][4], blk[MT][4];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) acc[mt][r] = 0.f;
-
-  // Software pipeline: the loads of the next KB blocks go to registers while
-  // the current ones are dotted from LDS; a thread's share of a stage is at
-  // most NCV/NSV/NQV/NDV vector, scale, q and d/s loads.
-  constexpr int NCV = (64 * 2 * KB + 255) / 256;  // 16-byte code loads
-  constexpr int NSV = (64 * KB + 255) / 256;      // scale loads
-  constexpr int NQV = (BM * 8 * KB + 255) / 256;  // 16-byte q loads
-  constexpr int NDV = (BM * 4 * KB + 255) / 256;  // d / s loads
-  u32x4 rc[NCV], rq[NQV];
-  uint16_t rsc[NSV];
-  float rd[NDV];
-  int rs[NDV];
-  auto fetch = [&](int kb0) {
-    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;
-#pragma unroll
-    for (int j = 0; j < NCV; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / (2 * KB), part = i - r * (2 * KB);  // part: 16-byte half of block part / 2
-      rc[j] = u32x4{0u, 0u, 0u, 0u};
-      if (i < 64 * 2 * KB && part < 2 * nkb) {
-        const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
-        const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
-        const int nc = nr < N ? nr : N - 1;
-        const uint8_t* cb = up ? a.up_codes : codes;
-        rc[j] = *reinterpret_cast<const u32x4*>(cb + (size_t)nc * rowb + kb0 * 32 + 16 * part);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NSV; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / KB, jj = i - r * KB;
-      rsc[j] = 0;
-      if (i < 64 * KB && jj < nkb) {
-        const bool up = MODE == BTF_GEMV_SWIGLU && r >= 32;
-        const int nr = n0 + (MODE == BTF_GEMV_SWIGLU ? (r & 31) : r);
-        const int nc = nr < N ? nr : N - 1;
-        const uint16_t* sb = up ? a.up_scales : scales;
-        rsc[j] = sb[(size_t)nc * nsc + kb0 + jj];
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NQV; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / (8 * KB), part = i - r * (8 * KB);
-      const int m = mb + r;
-      rq[j] = u32x4{0u, 0u, 0u, 0u};
-      if (i < BM * 8 * KB && part < 8 * nkb && m < a.nb)
-        rq[j] = *reinterpret_cast<const u32x4*>(a.q + (size_t)(a.m0 + m) * K + kb0 * 128 + 16 * part);
-    }
-#pragma unroll
-    for (int j = 0; j < NDV; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i / (4 * KB), sb = i - r * (4 * KB);
-      const int m = mb + r;
-      rd[j] = 0.f;
-      rs[j] = 0;
-      if (i < BM * 4 * KB && sb < 4 * nkb && m < a.nb) {
-        const size_t o = (size_t)(a.m0 + m) * nsub + kb0 * 4 + sb;
-        rd[j] = a.d[o];
-        rs[j] = a.s[o];
-      }
-    }
-  };
-  auto stage = [&]() {
-#pragma unroll
-    for (int j = 0; j < NCV; ++j) {
-      const int i = tid + 256 * j;
-      if (i < 64 * 2 * KB) {
-        const int r = i / (2 * KB), part = i - r * (2 * KB);
-        uint32_t* o = &cs[r * CS + 4 * part];
-        o[0] = rc[j].x; o[1] = rc[j].y; o[2] = rc[j].z; o[3] = rc[j].w;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NSV; ++j) {
-      const int i = tid + 256 * j;
-      if (i < 64 * KB) scs[(i / KB) * KB + (i - (i / KB) * KB)] = rsc[j];
-    }
-#pragma unroll
-    for (int j = 0; j < NQV; ++j) {
-      const int i = tid + 256 * j;
-      if (i < BM * 8 * KB) {
-        const int r = i / (8 * KB), part = i - r * (8 * KB);
-        uint32_t* o = &qsm[r * QS + 4 * part];
-        o[0] = rq[j].x; o[1] = rq[j].y; o[2] = rq[j].z; o[3] = rq[j].w;
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < NDV; ++j) {
-      const int i = tid + 256 * j;
-      if (i < BM * 4 * KB) {
-        const int r = i / (4 * KB), sb = i - r * (4 * KB);
-        dsm[sb][r] = rd[j];
-        nsm[sb][r] = -rs[j];
-      }
-    }
-  };
-
-  fetch(0);
-  for (int kb0 = 0; kb0 < nsc; kb0 += KB) {
-    const int nkb = nsc - kb0 < KB ? nsc - kb0 : KB;  // blocks this iteration
-    stage();
-    __syncthreads();
-    if (kb0 + KB < nsc) fetch(kb0 + KB);  // in flight while this stage is dotted
-
-    for (int kbi = 0; kbi < nkb; ++kbi) {
-    const int kb = kb0 + kbi;
-    // ---- 4 sub-blocks of MFMA ----
-#pragma unroll
-    for (int sb = 0; sb < 4; ++sb) {
-      const int sbx = 4 * kbi + sb;  // staged sub-block
-      const uint32_t word = cs[(16 * w + li) * CS + 2 * sbx + (t >> 1)];
-      const int sh = 4 * (t & 1);
-      const uint32_t lo = (word >> sh) & 0x03030303u;
-      const uint32_t hi = (word >> (sh + 2)) & 0x03030303u;
-      const long bfrag = (long)(((uint64_t)hi << 32) | lo);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const uint32_t* ap = &qsm[(16 * mt + li) * QS + 8 * sbx + 2 * t];
-        const long afrag = (long)(((uint64_t)ap[1] << 32) | ap[0]);
-        v4i cin;
-        cin[0] = nsm[sbx][16 * mt + 4 * t + 0];
-        cin[1] = nsm[sbx][16 * mt + 4 * t + 1];
-        cin[2] = nsm[sbx][16 * mt + 4 * t + 2];
-        cin[3] = nsm[sbx][16 * mt + 4 * t + 3];
-        const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag, cin, 0, 0, 0);
-        if constexpr (DUMP) {
-          const int n = n0 + 16 * w + li;
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int m = mb + 16 * mt + 4 * t + r;
-            if (m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + kb * 4 + sb] = I[r];
-          }
-        } else {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float dv = dsm[sbx][16 * mt + 4 * t + r];
-            blk[mt][r] = sb == 0 ? dv * (float)I[r] : fmaf(dv, (float)I[r], blk[mt][r]);
-          }
-        }
-      }
-    }
-    if constexpr (!DUMP) {
-      const float sc = h2f(scs[(16 * w + li) * KB + kbi]);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) acc[mt][r] = fmaf(sc, blk[mt][r], acc[mt][r]);
-    }
-    }  // kbi
-    __syncthreads();
-  }
-  if constexpr (DUMP) return;
-
-  // ---- epilogue ----
-  if constexpr (MODE == BTF_GEMV_SWIGLU) {
-    if (w >= 2) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) upx[(16 * (w - 2) + li) * BM + 16 * mt + 4 * t + r] = acc[mt][r];
-    }
-    __syncthreads();
-    if (w < 2) {
-      const int n = n0 + 16 * w + li;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = mb + 16 * mt + 4 * t + r;
-          if (m < a.nb && n < N) {
-            const float g = acc[mt][r];
-            const float u = upx[(16 * w + li) * BM + 16 * mt + 4 * t + r];
-            y[(size_t)(a.m0 + m) * ldy + n] = g / (1.0f + expf(-g)) * u;
-          }
-        }
-    }
-  } else {
-    const int n = n0 + 16 * w + li;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = mb + 16 * mt + 4 * t + r;
-        if (m < a.nb && n < N) {
-          float* o = &y[(size_t)(a.m0 + m) * ldy + n];
-          if constexpr (MODE == BTF_GEMV_ADD)
-            *o += acc[mt][r];
-          else
-            *o = acc[mt][r];
-        }
-      }
-  }
-}
-
 // K-split tile for batched decode (up to 32 activation rows): a workgroup of
 // NW waves owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows)
 // and BM activation rows, and wave w walks its 1/NW of the 128-column blocks,
 // staging its own codes, scales, q and d in a private LDS region (the codes
 // are permuted to int8 -1 / 0 / +1, so the MFMA yields I with accumulator 0
-// and s is not read). Four times as many workgroups as the 64-row tile and
-// 1/NW of the serial MFMA
-// chain per wave; the activation is re-read from L2 by each tile. Per wave
-// the row sums follow the 64-row kernel's order over its blocks, and the NW
-// wave partials are added in wave order: ((p0 + p1) + p2) + ...
+// and s is not read), KB blocks per round. The activation is re-read from L2
+// by each tile. Per wave the row sums follow the prefill tile's order over
+// its blocks (blk = d * I over a block's sub-blocks, acc += scale * blk per
+// block), and the NW wave partials are added in wave order: ((p0 + p1) + p2) + ...
 // TR = 2: the workgroup owns 32 weight rows (two 16-row tiles, each with its
 // gate and up rows), one Q8 block of the output for every activation row, so
 // it also writes the Q8 of its outputs (a.oq) with the q8 kernel's
@@ -594,9 +356,9 @@ void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st)
 // 16 * MW activation rows, 2 x MW MFMA tiles per 32-column sub-block from 2 B
 // and MW A fragments (swiglu: its two B tiles are the gate and up rows of the same
 // 16 outputs, so the epilogue stays in the lane). Per output the sums follow
-// the 64-row kernel's order: blk = d * I over the block's sub-blocks, then
+// this order: blk = d * I over the block's sub-blocks, then
 // acc += scale * blk per block.
-template <int MW, int KB, int MODE>
+template <int MW, int KB, int MODE, bool DUMP = false>
 __global__ void __launch_bounds__(256) gemm_pf_kernel(MfmaArgs a) {
   constexpr int BM = 32 * MW;
   constexpr int CS = 8 * KB + 1;
@@ -771,6 +533,13 @@ __global__ void __launch_bounds__(256) gemm_pf_kernel(MfmaArgs a) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             const v4i I = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], cin, 0, 0, 0);
+            if constexpr (DUMP) {  // the exact I of every (row, output, sub-block), as launched
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int m = mb + mr + 4 * t + r, n = n0 + srow[j] + li;
+                if (m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + (kb0 + kbi) * 4 + sb] = I[r];
+              }
+            }
 #pragma unroll
             for (int r = 0; r < 4; ++r)
               blk[j][mt][r] = sb == 0 ? dv[r] * (float)I[r] : fmaf(dv[r], (float)I[r], blk[j][mt][r]);
@@ -788,6 +557,7 @@ __global__ void __launch_bounds__(256) gemm_pf_kernel(MfmaArgs a) {
     }
     __syncthreads();
   }
+  if constexpr (DUMP) return;
 
 #pragma unroll
   for (int mt = 0; mt < MW; ++mt)
@@ -862,7 +632,7 @@ __device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds) {
 // q [BM][128 B] with the 16-byte chunk c of row r at slot c ^ (r & 7) (the A
 // fragments of 16 rows fall in 8 bank groups), codes [64][32 B], d [BM][4],
 // scales [64] in 4-byte slots. Same sums, in the same order, as gemm_pf_kernel.
-template <int MW, int S, int MODE>
+template <int MW, int S, int MODE, bool DUMP = false>
 __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
   constexpr int BM = 32 * MW;
   constexpr bool SW = MODE == BTF_GEMV_SWIGLU;
@@ -992,6 +762,17 @@ __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) I[mt][j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(afrag, bfrag[j], zero, 0, 0, 0);
       }
+      if constexpr (DUMP) {  // the exact I of every (row, output, sub-block), as launched
+#pragma unroll
+        for (int mt = 0; mt < MW; ++mt)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int rr = 0; rr < 4; ++rr) {
+              const int m = mb + 16 * MW * wm + 16 * mt + 4 * t + rr, n = n0 + srow[j] + li;
+              if (m < a.nb && n < N) a.dump[((size_t)(a.m0 + m) * N + n) * nsub + kb * 4 + sb] = I[mt][j][rr];
+            }
+      }
 #pragma unroll
       for (int mt = 0; mt < MW; ++mt) {
         const int mr = 16 * MW * wm + 16 * mt;
@@ -1016,6 +797,7 @@ __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
     }
   }
   wait_vm<0>();  // the trailing loads land before the workgroup's LDS is released
+  if constexpr (DUMP) return;
 
 #pragma unroll
   for (int mt = 0; mt < MW; ++mt)
@@ -1055,17 +837,6 @@ void by_mode_pf2(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_pf2_kernel<MW, S, BTF_GEMV_SWIGLU>), grid, dim3(256), 0, st, a);
 }
 
-template <int MT, bool DUMP>
-void by_mode(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
-  constexpr int KB = MT >= 4 ? 1 : 8;  // 8 blocks per round for one or two activation tiles
-  if (mode == BTF_GEMV_STORE)
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_STORE, DUMP>), grid, dim3(256), 0, st, a);
-  else if (mode == BTF_GEMV_ADD)
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_ADD, DUMP>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((gemm_mfma_kernel<MT, KB, BTF_GEMV_SWIGLU, DUMP>), grid, dim3(256), 0, st, a);
-}
-
 }  // namespace
 
 int mfma_rows_per_pass() { return 64; }
@@ -1074,7 +845,7 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
               hipStream_t st, const DevState& ds, const Q8* qout) {
   MfmaArgs a{};
   // up to 32 activation rows: the K-split 16-row tile (32 rows with a Q8
-  // output); more: the 64-row tile
+  // output); more: the prefill tile
   const bool ks = nb <= 32;
   if (qout && (!ks || dump)) return fail(BTF_ERR_ARGS, "gemm: a Q8 output needs at most 32 rows");
   const int rows_real = ks ? (qout ? 32 : 16) : mode == BTF_GEMV_SWIGLU ? 32 : 64;
@@ -1134,27 +905,35 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
       dmp ? by_waves_ks<2, true>(nw, mode, a, grid, st) : by_waves_ks<2, false>(nw, mode, a, grid, st);
     return launch_status("gemm_ks_kernel");
   }
-  if (!dmp && nb > 32) {
-    // 128 activation rows per tile while that still gives two workgroups per CU, else 64
-    const int cus = ds.cu_count > 0 ? ds.cu_count : 256;
-    const bool wide = (int64_t)tiles * ((nb + 127) / 128) >= 2 * cus;
-    // the LDS-direct ring loads d in 16-byte pieces
-    if ((reinterpret_cast<uintptr_t>(act.d) & 15) == 0) {
+  // 128 activation rows per tile while that still gives two workgroups per CU, else 64
+  const int cus = ds.cu_count > 0 ? ds.cu_count : 256;
+  const bool wide = (int64_t)tiles * ((nb + 127) / 128) >= 2 * cus;
+  const dim3 gw(tiles, (nb + 127) / 128), gn(tiles, (nb + 63) / 64);
+  // the LDS-direct ring loads d in 16-byte pieces
+  if ((reinterpret_cast<uintptr_t>(act.d) & 15) == 0) {
+    if (dmp) {  // the exact-I dump (btf_hip_gemv_i32_dump, one matrix): the same tile, writing I
       if (wide)
-        by_mode_pf2<4, 2>(mode, a, dim3(tiles, (nb + 127) / 128), st);  // 41 KB; 190 VGPRs: 2 workgroups per CU
+        hipLaunchKernelGGL((gemm_pf2_kernel<4, 2, BTF_GEMV_STORE, true>), gw, dim3(256), 0, st, a);
       else
-        by_mode_pf2<2, 3>(mode, a, dim3(tiles, (nb + 63) / 64), st);  // 34 KB: 4 workgroups per CU
-      return launch_status("gemm_pf2_kernel");
+        hipLaunchKernelGGL((gemm_pf2_kernel<2, 3, BTF_GEMV_STORE, true>), gn, dim3(256), 0, st, a);
+    } else if (wide) {
+      by_mode_pf2<4, 2>(mode, a, gw, st);  // 41 KB; 190 VGPRs: 2 workgroups per CU
+    } else {
+      by_mode_pf2<2, 3>(mode, a, gn, st);  // 34 KB: 4 workgroups per CU
     }
-    if (wide)
-      by_mode_pf<4>(mode, a, dim3(tiles, (nb + 127) / 128), st);
-    else
-      by_mode_pf<2>(mode, a, dim3(tiles, (nb + 63) / 64), st);
-    return launch_status("gemm_pf_kernel");
+    return launch_status("gemm_pf2_kernel");
   }
-  // left: the exact-I dump (btf_hip_gemv_i32_dump) of more than 32 rows
-  by_mode<4, true>(mode, a, grid, st);
-  return launch_status("gemm_mfma_kernel");
+  if (dmp) {
+    if (wide)
+      hipLaunchKernelGGL((gemm_pf_kernel<4, 1, BTF_GEMV_STORE, true>), gw, dim3(256), 0, st, a);
+    else
+      hipLaunchKernelGGL((gemm_pf_kernel<2, 1, BTF_GEMV_STORE, true>), gn, dim3(256), 0, st, a);
+  } else if (wide) {
+    by_mode_pf<4>(mode, a, gw, st);
+  } else {
+    by_mode_pf<2>(mode, a, gn, st);
+  }
+  return launch_status("gemm_pf_kernel");
 }
 
 }  // namespace btfhip

@@ -42,6 +42,8 @@
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <type_traits>
 #include <vector>
@@ -265,14 +267,29 @@ __device__ __forceinline__ T* sgpr_ptr(T* p) {
   return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
 }
 
+// Unit placement and the word offsets of every global store the kernel
+// makes. Host code uses the same functions (btf_hip_step_audit replays the
+// stores of a program over every workgroup and checks each against the
+// buffers the program owns or was given).
 // First workgroup-local unit of an op: units u with u % G == (wg - rot) mod G.
-__device__ __forceinline__ int first_unit(int rot, int wg, int G) {
+__host__ __device__ __forceinline__ int first_unit(int rot, int wg, int G) {
   const int f = wg - rot;
   return f < 0 ? f + G : f;
 }
-__device__ __forceinline__ int units_of(int units, int first, int G) {
+__host__ __device__ __forceinline__ int units_of(int units, int first, int G) {
   return first < units ? (units - 1 - first) / G + 1 : 0;
 }
+// Output row (fp32 word) of value j of a 32-value unit.
+__host__ __device__ __forceinline__ int unit_row(int unit, int j) { return unit * 32 + j; }
+// First Q8 LL word of 32-value block `blk` (8 q words, d, s).
+__host__ __device__ __forceinline__ size_t q8_block_word(int blk) { return (size_t)blk * kWordsPerBlock; }
+// LL words of block `blk`'s sum of squares (low, high half of the double):
+// after the vector's N fp32 words.
+__host__ __device__ __forceinline__ size_t sq_word(int N, int blk) { return (size_t)N + 2 * (size_t)blk; }
+// First value of lane `lane`'s 16 of 1024-value unit `unit` (an embedding's output).
+__host__ __device__ __forceinline__ int slice_col(int unit, int lane) { return unit * kSliceVals + 16 * lane; }
+// A workgroup's greedy-pick key: 2 LL words.
+__host__ __device__ __forceinline__ size_t pick_word(int wg) { return 2 * (size_t)wg; }
 
 // ---------------------------------------------------------------- input fetch
 template <class LT>
@@ -1088,7 +1105,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
 // Publish one 32-value unit held by a half-wave: fp32 LL words, plain output
 // and the Q8 LL words.
 __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, float v, bool valid, uint32_t tag) {
-  const int row = unit * 32 + j;
+  const int row = unit_row(unit, j);
   float* out_plain = sgpr_ptr(op.out_plain);
   uint64_t* out_f32 = sgpr_ptr(op.out_f32);
   uint64_t* out_q8 = sgpr_ptr(op.out_q8);
@@ -1102,7 +1119,7 @@ __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, f
     const uint32_t b = (uint32_t)(q & 0xff) << (8 * (j & 3));
     uint32_t w = b | (uint32_t)dpp_i<0xB1>((int)b);  // quad_perm(1,0,3,2)
     w |= (uint32_t)dpp_i<0x4E>((int)w);              // quad_perm(2,3,0,1)
-    uint64_t* dst = out_q8 + (size_t)unit * kWordsPerBlock;
+    uint64_t* dst = out_q8 + q8_block_word(unit);
     if ((j & 3) == 0) ll_store(dst + (j >> 2), ((uint64_t)tag << 32) | w);
     if (j == 0) ll_store(dst + 8, ((uint64_t)tag << 32) | __float_as_uint(d));
     if (j == 1) ll_store(dst + 9, ((uint64_t)tag << 32) | (uint32_t)s);
@@ -1124,7 +1141,7 @@ __device__ __forceinline__ void publish_unit(const OpDev& op, int unit, int j, f
         __longlong_as_double((long long)(((uint64_t)__float_as_uint(hhi) << 32) | __float_as_uint(lhi)));
     if (j == 0) {
       const uint64_t b = __double_as_longlong(t);
-      uint64_t* dst = out_f32 + sgpr(op.N) + 2 * unit;
+      uint64_t* dst = out_f32 + sq_word(sgpr(op.N), unit);
       ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)b);
       ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(b >> 32));
     }
@@ -1153,7 +1170,7 @@ __device__ __forceinline__ void publish_slice(const OpDev& op, int c0, int lane,
   if (sgpr(op.out_sq)) {
     const uint64_t b = __double_as_longlong(pair_sumsq(v));
     if (!h) {
-      uint64_t* dst = out_f32 + sgpr(op.N) + 2 * blk;
+      uint64_t* dst = out_f32 + sq_word(sgpr(op.N), blk);
       ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)b);
       ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(b >> 32));
     }
@@ -1163,7 +1180,7 @@ __device__ __forceinline__ void publish_slice(const OpDev& op, int c0, int lane,
     float d;
     int s;
     q8_pair(v, qw, d, s);
-    uint64_t* dst = out_q8 + (size_t)blk * kWordsPerBlock;
+    uint64_t* dst = out_q8 + q8_block_word(blk);
 #pragma unroll
     for (int k = 0; k < 4; ++k) ll_store(dst + 4 * h + k, ((uint64_t)tag << 32) | qw[k]);
     if (!h) {
@@ -1183,7 +1200,7 @@ __device__ __forceinline__ void io_embed(const OpDev& op, const PrepRegs& pd, in
   const gptr<uint32_t> rowc = as_global(reinterpret_cast<const uint32_t*>(sgpr_ptr(op.codes) + (size_t)tok * (size_t)(E / 4)));
   const gptr<uint16_t> rows = as_global(sgpr_ptr(op.scales) + (size_t)tok * (size_t)(E / 128));
   for (int u = first_unit(sgpr(op.rot), wg, G) + iw * G; u < units; u += kIW * G) {
-    const int c0 = u * kSliceVals + 16 * lane;
+    const int c0 = slice_col(u, lane);
     const uint32_t w = rowc[c0 >> 4];
     const float sc = h2f(rows[c0 >> 7]);
     float v[16];
@@ -1207,7 +1224,7 @@ __device__ __forceinline__ void io_quantize(const OpDev& op, int wg, int G, int 
   const int N = sgpr(op.N), units = sgpr(op.units);
   const float* src = sgpr_ptr(static_cast<const float*>(op.src));
   for (int u = first_unit(sgpr(op.rot), wg, G) + half * G; u < units; u += nhalves * G) {
-    const int row = u * 32 + j;
+    const int row = unit_row(u, j);
     const bool valid = row < N;
     const float v = valid ? *(const __attribute__((address_space(1))) float*)(src + row) : 0.f;
     publish_unit(op, u, j, v, valid, tag);
@@ -1299,7 +1316,7 @@ __device__ __forceinline__ void io_publish(const OpDev& op, LT& L, int wg, int G
     asm volatile("" ::: "memory");
     if (j < LT::kCW) __hip_atomic_store(&L.ucnt[j][ui], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     const int unit = first + ui * G;
-    const int row = unit * 32 + j;
+    const int row = unit_row(unit, j);
     const bool valid = row < N;
     float v;
     if (mode == BTF_GEMV_SWIGLU) {
@@ -1427,7 +1444,7 @@ __device__ __forceinline__ void io_waves(Lds<kFull>& L, int nops, Ctl* ctl, uint
                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (kFull && sgpr(op.argmax) && io0 && first_lane(iol)) {  // this workgroup's pick key: the larger of the two I/O waves'
       const uint64_t k = key_max(L.argk[0], L.argk[1]);
-      uint64_t* dst = sgpr_ptr(as_const(sgpr_ptr(L.head))->parts) + 2 * wg;
+      uint64_t* dst = sgpr_ptr(as_const(sgpr_ptr(L.head))->parts) + pick_word(wg);
       const uint32_t tag = base_tag + sgpr(op.my_tag);
       ll_store(dst, ((uint64_t)tag << 32) | (uint32_t)k);
       ll_store(dst + 1, ((uint64_t)tag << 32) | (uint32_t)(k >> 32));
@@ -1520,11 +1537,21 @@ struct StepProgram {
   bool full = false;            // any prep, embedding or pick: the kFull kernel
   int guards = 0;               // ops that keep a write-after-read wait (not implied by the data flow)
   std::vector<void*> bufs;      // every device buffer the program owns
+  // A plan built without a device (btf_hip_step_audit): the buffers are host
+  // memory, and the device program is kept here instead of uploaded.
+  bool host = false;
+  std::vector<size_t> buf_bytes;
+  std::vector<OpDev> plan_ops;
+  std::vector<PrepDev> plan_preps;
+  HeadDev plan_head{};
 };
 
 void step_destroy(StepProgram* P) {
   if (!P) return;
-  for (void* p : P->bufs) (void)hipFree(p);
+  for (void* p : P->bufs) {
+    if (P->host) std::free(p);
+    else (void)hipFree(p);
+  }
   delete P;
 }
 
@@ -1624,11 +1651,16 @@ int step_validate(const btf_step_vec* vecs, int nvec, const btf_step_gemv* gemvs
   return step_validate_ops(vecs, nvec, ops.data(), ngemv);
 }
 
-int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops, int nuops, StepProgram** out,
-                    const DevState& ds) {
+namespace {
+// Builds a program for a grid of G workgroups. host_G > 0: without a device
+// (the buffers in host memory, the program kept in P instead of uploaded).
+int step_build(const btf_step_vec* vecs, int nvec, const btf_step_op* uops, int nuops, StepProgram** out,
+               const DevState* ds, int host_G) {
+  const bool host = host_G > 0;
   if (const int rc = step_validate_ops(vecs, nvec, uops, nuops)) return rc;
-  if (const int rc = step_check_residency(ds)) return rc;
-  const int G = ds.cu_count;
+  if (!host)
+    if (const int rc = step_check_residency(*ds)) return rc;
+  const int G = host ? host_G : ds->cu_count;
   if (G > 256) return fail(BTF_ERR_DEVICE, "step: more than 256 CUs");
   // ---- versions of every vector over the program. Version 0 of a vector
   // read before any write is its user data, published by a prologue op;
@@ -1684,11 +1716,17 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     if (!versions[v].empty()) final_writer[v] = versions[v].back().writer;
   StepProgram* P = new StepProgram();
   P->G = G;
+  P->host = host;
   auto alloc = [&](size_t bytes) -> void* {
     void* p = nullptr;
-    if (hipMalloc(&p, bytes) != hipSuccess) return nullptr;
+    if (host) {
+      if (!(p = std::calloc(bytes, 1))) return nullptr;
+    } else if (hipMalloc(&p, bytes) != hipSuccess) {
+      return nullptr;
+    }
     P->bufs.push_back(p);
-    if (hipMemset(p, 0, bytes) != hipSuccess) return nullptr;
+    P->buf_bytes.push_back(bytes);
+    if (!host && hipMemset(p, 0, bytes) != hipSuccess) return nullptr;
     return p;
   };
   auto bail = [&](int code, const char* msg) {
@@ -1929,23 +1967,27 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
       for (int r : v0.old_readers) last = std::max(last, r);
       if (last >= 0 && last != i) war = std::max(war, dev_of[last]);
     }
-    // What this op's writers learn from its input: they read all of it
-    // before publishing any unit (a unit spans every slice), so it counts for
-    // this op's own guard.
+    // What this op's writers learn from its input: they read all of the
+    // first K values before publishing any unit (a unit spans every slice),
+    // so it counts for this op's own guard -- but only the writers of the
+    // input units below K are observed (an op without a prep may read a
+    // prefix of a longer vector).
     {
       const int x = (int)o.in_tag - 1;  // input producer
       const int px = x < (int)prev_gemv.size() ? prev_gemv[x] : -1;
       if (ops[x].kind == 1) {
+        const int nread = std::min(ops[x].units, (o.K + 31) / 32);
+        auto observed = [&](int w) { return (w - ops[x].rot + G) % G < nread; };
         int a_in = ax[x];
         bool all_write = px >= 0;
-        for (int w = 0; w < G && all_write; ++w) all_write = owns(ops[x], w);
+        for (int w = 0; w < G && all_write; ++w) all_write = observed(w);
         if (all_write) a_in = std::max(a_in, px);
         for (int v = 0; v < G; ++v) {
           if (!owns(o, v)) continue;
           allk[v] = std::max(allk[v], a_in);
           if (px >= 0)
             for (int w = 0; w < G; ++w)
-              if (owns(ops[x], w)) known[(size_t)v * G + w] = std::max(known[(size_t)v * G + w], px);
+              if (observed(w)) known[(size_t)v * G + w] = std::max(known[(size_t)v * G + w], px);
         }
       }
     }
@@ -2025,7 +2067,9 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
   }
   for (size_t t = 0; t < run_tables.size(); ++t) {
     int* d = static_cast<int*>(alloc(run_tables[t].size() * sizeof(int)));
-    if (!d || hipMemcpy(d, run_tables[t].data(), run_tables[t].size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess)
+    if (d && host) std::memcpy(d, run_tables[t].data(), run_tables[t].size() * sizeof(int));
+    if (!d || (!host && hipMemcpy(d, run_tables[t].data(), run_tables[t].size() * sizeof(int),
+                                  hipMemcpyHostToDevice) != hipSuccess))
       return bail(BTF_ERR_LAUNCH, "step: gather table upload failed");
     preps[run_of[t]].runs = d;
   }
@@ -2040,6 +2084,14 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
       !(P->d_head = static_cast<HeadDev*>(alloc(sizeof(HeadDev)))))
     return bail(BTF_ERR_LAUNCH, "step: device allocation failed");
   const Ctl c0{1u, 0u, 0u, 0u};
+  if (host) {
+    P->plan_ops = ops;
+    P->plan_preps = preps;
+    P->plan_head = head;
+    *P->d_ctl = c0;
+    *out = P;
+    return BTF_OK;
+  }
   if (hipMemcpy(P->d_ops, ops.data(), ops.size() * sizeof(OpDev), hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(P->d_ctl, &c0, sizeof c0, hipMemcpyHostToDevice) != hipSuccess ||
       hipMemcpy(P->d_preps, preps.data(), preps.size() * sizeof(PrepDev), hipMemcpyHostToDevice) != hipSuccess ||
@@ -2047,6 +2099,125 @@ int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops,
     return bail(BTF_ERR_LAUNCH, "step: program upload failed");
   (void)hipGetDevice(&P->device);
   *out = P;
+  return BTF_OK;
+}
+}  // namespace
+
+int step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* uops, int nuops, StepProgram** out,
+                    const DevState& ds) {
+  return step_build(vecs, nvec, uops, nuops, out, &ds, 0);
+}
+
+// The global stores of a program's launch, replayed on the host over every
+// workgroup with the kernel's own placement and address functions
+// (first_unit, units_of, unit_row, q8_block_word, sq_word, slice_col,
+// pick_word) and the store pattern of publish_unit, publish_slice,
+// io_quantize, io_embed, io_publish, io_waves, io_pick and the kernel's
+// epilogue; each store must lie inside a buffer the program owns or one it
+// was given (a vector's data, the pick's token and position).
+int step_audit(const btf_step_vec* vecs, int nvec, const btf_step_op* uops, int nuops, int G, btf_step_audit* res) {
+  if (G <= 0 || G > 256) return fail(BTF_ERR_ARGS, "step audit: G must be in 1..256");
+  StepProgram* P = nullptr;
+  if (const int rc = step_build(vecs, nvec, uops, nuops, &P, nullptr, G)) return rc;
+  struct Range {
+    uintptr_t a, b;
+    const char* what;
+  };
+  std::vector<Range> rs;
+  for (size_t i = 0; i < P->bufs.size(); ++i)
+    rs.push_back({reinterpret_cast<uintptr_t>(P->bufs[i]), reinterpret_cast<uintptr_t>(P->bufs[i]) + P->buf_bytes[i],
+                  "program buffer"});
+  for (int v = 0; v < nvec; ++v)
+    if (vecs[v].data)
+      rs.push_back({reinterpret_cast<uintptr_t>(vecs[v].data),
+                    reinterpret_cast<uintptr_t>(vecs[v].data) + 4 * (size_t)vecs[v].n, "vector data"});
+  const HeadDev& head = P->plan_head;
+  if (head.present) {
+    rs.push_back({reinterpret_cast<uintptr_t>(head.tok_out), reinterpret_cast<uintptr_t>(head.tok_out) + 4, "token"});
+    if (head.pos)
+      rs.push_back({reinterpret_cast<uintptr_t>(head.pos), reinterpret_cast<uintptr_t>(head.pos) + 4, "position"});
+  }
+  std::sort(rs.begin(), rs.end(), [](const Range& x, const Range& y) { return x.a < y.a; });
+  *res = btf_step_audit{};
+  res->ops = P->nops;
+  res->guards = P->guards;
+  res->full = P->full ? 1 : 0;
+  auto store = [&](const void* p, size_t bytes, int op, int wg, const char* site) {
+    ++res->stores;
+    const uintptr_t a = reinterpret_cast<uintptr_t>(p);
+    auto it = std::upper_bound(rs.begin(), rs.end(), a, [](uintptr_t x, const Range& r) { return x < r.a; });
+    if (it != rs.begin() && a >= std::prev(it)->a && a + bytes <= std::prev(it)->b) return;
+    if (res->outside++ == 0)
+      std::snprintf(res->first_outside, sizeof res->first_outside, "op %d workgroup %d: %s, %zu bytes at %p", op, wg,
+                    site, bytes, p);
+  };
+  auto unit_stores = [&](const OpDev& o, int d, int wg, int unit) {  // publish_unit, j = 0..31
+    for (int j = 0; j < 32; ++j) {
+      const int row = unit_row(unit, j);
+      const bool valid = row < o.N;
+      if (valid && o.out_plain) store(o.out_plain + row, 4, d, wg, "plain output");
+      if (valid && o.out_f32) store(o.out_f32 + row, 8, d, wg, "fp32 LL word");
+      if (o.out_q8) {
+        uint64_t* dst = o.out_q8 + q8_block_word(unit);
+        if ((j & 3) == 0) store(dst + (j >> 2), 8, d, wg, "Q8 q word");
+        if (j == 0) store(dst + 8, 8, d, wg, "Q8 d word");
+        if (j == 1) store(dst + 9, 8, d, wg, "Q8 s word");
+      }
+      if (o.out_sq && j == 0) {
+        store(o.out_f32 + sq_word(o.N, unit), 8, d, wg, "sum of squares (low)");
+        store(o.out_f32 + sq_word(o.N, unit) + 1, 8, d, wg, "sum of squares (high)");
+      }
+    }
+  };
+  for (int wg = 0; wg < G; ++wg) {
+    for (int d = 0; d < P->nops; ++d) {
+      const OpDev& o = P->plan_ops[(size_t)d];
+      const int first = first_unit(o.rot, wg, G);
+      if (o.kind == 0) {  // io_quantize: half-waves 0..3, units first + h G + 4 G t
+        for (int h = 0; h < 2 * kIW; ++h)
+          for (int u = first + h * G; u < o.units; u += 2 * kIW * G) unit_stores(o, d, wg, u);
+      } else if (o.kind == 2) {  // io_embed: I/O waves 0..1, units first + w G + 2 G t; publish_slice per lane
+        for (int iw = 0; iw < kIW; ++iw)
+          for (int u = first + iw * G; u < o.units; u += kIW * G)
+            for (int lane = 0; lane < 64; ++lane) {
+              const int c0 = slice_col(u, lane), blk = c0 >> 5, h = lane & 1;
+              if (o.out_plain) store(o.out_plain + c0, 64, d, wg, "plain output (slice)");
+              if (o.out_f32)
+                for (int i = 0; i < 16; ++i) store(o.out_f32 + c0 + i, 8, d, wg, "fp32 LL word (slice)");
+              if (o.out_sq && !h) {
+                store(o.out_f32 + sq_word(o.N, blk), 8, d, wg, "sum of squares (slice)");
+                store(o.out_f32 + sq_word(o.N, blk) + 1, 8, d, wg, "sum of squares (slice)");
+              }
+              if (o.out_q8) {
+                uint64_t* dst = o.out_q8 + q8_block_word(blk);
+                for (int k = 0; k < 4; ++k) store(dst + 4 * h + k, 8, d, wg, "Q8 q word (slice)");
+                if (!h) {
+                  store(dst + 8, 8, d, wg, "Q8 d word (slice)");
+                  store(dst + 9, 8, d, wg, "Q8 s word (slice)");
+                }
+              }
+            }
+      } else {  // io_publish: local units ui = half + 4 t of the workgroup's nunits
+        const int nunits = units_of(o.units, first, G);
+        for (int half = 0; half < 2 * kIW; ++half)
+          for (int ui = half; ui < nunits; ui += 2 * kIW) unit_stores(o, d, wg, first + ui * G);
+        if (o.count_reads) store(P->d_cnt + wg, 4, d, wg, "progress word");
+        if (o.argmax) {
+          store(head.parts + pick_word(wg), 8, d, wg, "pick key (low)");
+          store(head.parts + pick_word(wg) + 1, 8, d, wg, "pick key (high)");
+        }
+      }
+    }
+    if (wg == 0 && head.present) {  // io_pick
+      store(head.tok_out, 4, P->nops, wg, "token");
+      if (head.pos) store(head.pos, 4, P->nops, wg, "position");
+    }
+    // set_abort, the end-of-step count and the epoch advance
+    store(&P->d_ctl->error, 4, P->nops, wg, "control: error");
+    store(&P->d_ctl->done, 4, P->nops, wg, "control: done");
+    store(&P->d_ctl->epoch, 4, P->nops, wg, "control: epoch");
+  }
+  step_destroy(P);
   return BTF_OK;
 }
 

@@ -273,6 +273,27 @@ typedef struct btf_step_op {
 } btf_step_op;
 int btf_hip_step_create_ops(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, btf_step_t* out);
 
+/* Test hook, host only (no device is touched): builds the program of
+ * btf_hip_step_create_ops for a grid of G workgroups (1..256), its own
+ * buffers in host memory, and replays every global store a launch of it
+ * makes -- each workgroup's published units (fp32 and Q8 LL words, block
+ * sums of squares, plain outputs), progress words, pick keys, the token,
+ * the position and the control block -- with the kernel's own placement and
+ * address functions, checking that each lies inside a buffer the program
+ * owns or was given (a vector's data, d_tok_out, d_pos). No counterpart in
+ * the reference; it plays the part of its build-time kernel resource check
+ * (cmake/check_kernel_resources.cmake:15-61) for the step kernel's stores. */
+typedef struct btf_step_audit {
+  int64_t stores;           /* stores checked */
+  int64_t outside;          /* stores outside every such buffer (0: none) */
+  int ops;                  /* device ops (prologue + embeddings + GEMVs) */
+  int guards;               /* as btf_hip_step_guards */
+  int full;                 /* 1: the kernel instance with preps, embedding and pick */
+  char first_outside[160];  /* the first stray store, described */
+} btf_step_audit;
+int btf_hip_step_audit(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, int G,
+                       btf_step_audit* out);
+
 /* ---- load path: GGUF reader -> pinned double-buffered staging -> repack --
  * The reference decoder reads its model with bd::Gguf
  * (ref/bonsai-decoder/include/bd/gguf.hpp:49-85, src/gguf.cpp:73-147),

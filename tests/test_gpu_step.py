@@ -201,6 +201,51 @@ def test_step_reordered_chain_and_war(hip, oracle):
     prog.close()
 
 
+def test_step_prefix_reader_keeps_its_guard(hip, oracle):
+    """An op reading the first 1024 values of a vector that every workgroup
+    wrote (8192 values) overwrites a Q8 buffer whose earlier version other
+    workgroups may still be reading: the program keeps that write-after-read
+    wait (the host analysis credits only the writers of the prefix) and the
+    launch equals the op-by-op launches, twice in a row."""
+    torch = _torch()
+    G = hip.GemvMode
+    rng = np.random.default_rng(41)
+    m = lambda N, K: host_mat(oracle, rng, N, K)
+    spec = [(1024, 1024, 1, 2, G.kStore), (1024, 1024, 4, 1, G.kStore), (1024, 1024, 1, 2, G.kStore),
+            (1024, 1024, 4, 1, G.kStore), (1024, 1024, 1, 2, G.kStore), (1024, 8192, 4, 0, G.kStore),
+            (1024, 1024, 0, 1, G.kStore), (1024, 1024, 1, 3, G.kStore)]
+    ops = []
+    for K, N, i, o, mode in spec:
+        w = m(N, K)
+        ops.append(hip.StepGemv(mode, K, N, w.codes, w.scales, i, o))
+    lengths = (8192, 1024, 1024, 1024, 1024)
+    inputs = [rng.standard_normal(n).astype(np.float32) for n in lengths]
+
+    def vectors():
+        t = [dev(a) for a in inputs]
+        return [hip.StepVec(int(x.numel()), x) for x in t], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    full_ops = list(ops)
+    full_ops[6] = hip.StepGemv(G.kStore, 8192, 1024, *(lambda w: (w.codes, w.scales))(m(1024, 8192)), 0, 1)
+    assert prog.guards() == hip.step_audit(vecs, ops)["guards"] >= 1
+    assert hip.step_audit(vecs, full_ops)["guards"] == prog.guards() - 1
+    for rep in range(2):
+        if rep:
+            for x, a in zip(t, inputs):
+                x.copy_(dev(a))
+        prog.launch(stream())
+        torch.cuda.synchronize()
+        assert prog.error() == 0
+        _, s = vectors()
+        run_sequential(hip, ops, s)
+        for k, (a, b) in enumerate(zip(t, s)):
+            ga, gb = host(a), host(b)
+            assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), f"launch {rep} vector {k}"
+    prog.close()
+
+
 def test_step_each_op_vs_oracle(hip, oracle):
     """Every op against the oracle on the step's own input vector: a chain in
     which each op writes a vector of its own (all observable), so a Q8 input

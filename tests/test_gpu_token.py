@@ -307,3 +307,95 @@ def test_step_prep_every_transform_block(hip, oracle, block):
     assert_close_1e3(host(t[1]), oracle.gemv(W1[0], W1[1], K, q, d, s_)[0], f"block {block}: GEMV 1")
     q, d, s_, _ = oracle.prep(host(t[1])[None, :], None, 0.0, block, 64, 12, 4, None)
     assert_close_1e3(host(t[2]), oracle.gemv(W2[0], W2[1], N1, q, d, s_)[0], f"block {block}: GEMV 2")
+
+
+def test_whole_token_27b_bench_program(hip, oracle):
+    """The benchmark's whole-token program at the 27B shapes (the bench's own
+    Setup and token_ops): the embedding (inverse FWHT 1024 + signs), 64 x
+    (QKV with RMSNorm + FWHT 1024 + signs, o += with FWHT + signs, gate+up
+    swiglu with RMSNorm + FWHT + signs, down += with FWHT + signs), the
+    5120->248320 output projection with RMSNorm + FWHT + signs, the greedy
+    pick and the position counter, in one launch.
+      * Every vector, the token and the position are bit-exact against the
+        same ops launched one by one (launch_embed, launch_prep + launch_gemv,
+        launch_argmax, launch_pos_add: src/cuda/gpu_decoder.cu:401-421,
+        452-486), over two launches (the second decodes the first's pick).
+      * Sampled prepped ops of the op-by-op run -- layers 0, 31 and 63 and
+        every 16th row of the output projection -- are within 1e-3 of the
+        oracle's prep + emulator GEMV on their own fp32 inputs, and each
+        launch's token is the oracle's greedy pick over its logits."""
+    import os
+    import sys
+    torch = _torch()
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    if root not in sys.path:
+        sys.path.insert(0, root)
+    import bench
+    L, E, F, V = bench.LAYERS, bench.E, bench.F, bench.V
+    S = bench.Setup(hip, torch, L, with_embed=True)
+    T = bench.Token(S, L)
+    # the op-by-op twin: its own token, position and vectors
+    z = lambda n: torch.zeros(n, dtype=torch.float32, device="cuda")
+    tok2, pos2 = dev(np.array([T.tok0], np.int32)), torch.zeros(1, dtype=torch.int32, device="cuda")
+    twin = [z(E), z(bench.QKV), T.att.clone(), z(F), z(V)]
+    ops = T.ops()
+    T.tok.fill_(T.tok0)
+    T.pos.zero_()
+    prog = hip.StepProgram(T.vecs(), ops)
+    sample = (0, 31, 63)
+    G = hip.GemvMode
+    try:
+        for launch in range(2):
+            prog.launch(stream())
+            torch.cuda.synchronize()
+            assert prog.error() == 0
+            seen = {}
+            tops = bench.token_ops(hip, S.weights, L, tok2, pos2, T.hx,
+                                   [tuple(T.nw(w) for w in ln) for ln in T.norm], T.signs,
+                                   T.nw(T.out_norm), T.out_signs, T.emb_signs)
+            gi = 0
+            for op in tops:
+                keep = isinstance(op, hip.StepGemv) and (gi // 4 in sample or gi == 4 * L)
+                if keep:
+                    seen[gi] = [host(twin[op.in_vec]).copy(), host(twin[op.out_vec]).copy()]
+                run_ops_sequential(hip, [op], twin)
+                if keep:
+                    seen[gi].append(host(twin[op.out_vec]).copy())
+                gi += isinstance(op, hip.StepGemv)
+            for name, a, b in zip(("res", "qkv", "att", "h", "logits"), T.vecs(), twin):
+                ga, gb = host(a.data), host(b)
+                assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), \
+                    f"launch {launch} {name}: step != op-by-op (max diff {np.max(np.abs(ga - gb)):.3e})"
+            tok_step, tok_seq = int(host(T.tok)[0]), int(host(tok2)[0])
+            assert tok_step == tok_seq and int(host(T.pos)[0]) == int(host(pos2)[0]) == launch + 1
+            logits = host(T.logits)
+            assert np.isfinite(logits).all()
+            assert tok_step == oracle.argmax(logits)
+            # sampled ops against the oracle
+            for gi, (xin, old, got) in sorted(seen.items()):
+                l, k = divmod(gi, 4)
+                if gi == 4 * L:
+                    normw, sg, key, K, mode = T.out_norm, T.out_signs, ("output", L), E, "store"
+                else:
+                    na, nf = T.norm[l]
+                    sq, so_, sgu, sd = T.signs[l]
+                    normw, sg, key, K, mode = [(na, sq, ("qkv", l), E, "store"), (None, so_, ("o", l), E, "add"),
+                                               (nf, sgu, ("gate", l), E, "swiglu"),
+                                               (None, sd, ("down", l), F, "add")][k]
+                hn = host(normw) if normw is not None else None
+                q, d, s_, _ = oracle.prep(xin[None, :], hn, 1e-6, 1024, 0, 0, 0, host(sg))
+                if mode == "swiglu":
+                    want = oracle.swiglu(oracle.gemv(*S.host_mat("gate", l), K, q, d, s_),
+                                         oracle.gemv(*S.host_mat("up", l), K, q, d, s_))[0]
+                    assert_close_1e3(got, want, f"launch {launch} layer {l} gate+up")
+                elif gi == 4 * L:
+                    rows = np.arange(0, V, 16)
+                    c, sc = S.host_mat("output", L)
+                    want = oracle.gemv(np.ascontiguousarray(c[rows]), np.ascontiguousarray(sc[rows]), K, q, d, s_)[0]
+                    assert_close_1e3(got[rows], want, f"launch {launch} output projection (every 16th row)")
+                else:
+                    want = oracle.gemv(*S.host_mat(*key), K, q, d, s_, y=old[None, :].copy() if mode == "add" else None,
+                                       add=mode == "add")[0]
+                    assert_close_1e3(got, want, f"launch {launch} layer {l} {key[0]}")
+    finally:
+        prog.close()
