@@ -119,14 +119,16 @@ int64_t btf_hip_argmax_part_bytes(int V);
 int btf_hip_launch_argmax(const float* logits, int V, void* part, int* d_tok_out, btf_stream_t stream);
 
 /* No counterpart in the reference: launch_argmax without the `part`
- * workspace, for callers that cannot allocate (code under graph capture that
- * may not call hipMalloc, tight serving loops, harnesses that forbid it). Its
- * scratch is a file-scope static device array of 256 8-byte keys (2 KiB per
- * GPU, held until the process ends), enough for any V; the library takes its
- * address per device in btf_hip_kernels_init. Allocates nothing. Every call
- * on a GPU shares that GPU's scratch: calls that overlap on one GPU (on
- * different streams, or from several threads) race. Same result as
- * btf_hip_launch_argmax. */
+ * workspace, for callers that cannot allocate (tight serving loops,
+ * harnesses that forbid hipMalloc). Its scratch is a file-scope static
+ * device array of 256 8-byte keys (2 KiB per GPU, held until the process
+ * ends), enough for any V; the library takes its address per device in
+ * btf_hip_kernels_init. Allocates nothing. Every call on a GPU shares that
+ * GPU's scratch, so calls must be serialized on that GPU: two calls that may
+ * overlap (on different streams, from several threads, or a captured graph
+ * replayed while another call or replay runs) race and can return a wrong
+ * token. Issue every call -- and replay every graph that holds one -- on one
+ * stream. Same result as btf_hip_launch_argmax. */
 int btf_hip_launch_argmax_noalloc(const float* logits, int V, int* d_tok_out, btf_stream_t stream);
 
 /* Replaces btf::cuda::launch_pos_add (kernels.cuh:92): *d_pos += M. */
