@@ -635,6 +635,33 @@ def run_batched_sub(S: Setup, M, layers, steps, warmup, traffic_tab):
     return out
 
 
+def stream_ceiling(S: Setup, reps=5):
+    """The practical HBM read ceiling: btf_hip_stream_read (non-temporal
+    16-byte loads, as the GEMV kernels read their weights) over the weight
+    arena (6 GB, beyond the 256 MB memory-side cache), HIP events on its
+    stream."""
+    hip, torch = S.hip, S.torch
+    nbytes = S.arena_bytes // 16 * 16
+    sink = torch.zeros(1, dtype=torch.int32, device="cuda")
+    s = torch.cuda.Stream()
+    hip.stream_read(S.arena, nbytes, sink, s.cuda_stream)
+    e0, e1 = hip.Event(), hip.Event()
+    try:
+        e0.record(s)
+        for _ in range(reps):
+            hip.stream_read(S.arena, nbytes, sink, s.cuda_stream)
+        e1.record(s)
+        s.synchronize()
+        ms = e0.elapsed_ms(e1) / reps
+    finally:
+        e0.close()
+        e1.close()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"what": "btf_hip_stream_read: non-temporal 16-byte loads over the weight arena (the practical HBM "
+                    "read ceiling)", "bytes": nbytes, "ms": round(ms, 4), "GBs": round(gbs, 1),
+            "frac_of_8TBs": round(gbs / HBM_PEAK_GBS, 4)}
+
+
 def time_graph(hip, torch, fn, reps, warmup):
     """Capture fn(stream) in one graph, replay warmup + reps times; returns ms
     per replay. The graph and the events are released before returning."""
@@ -729,10 +756,12 @@ def cpu_info():
 def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
     """The reference CPU emulator's GEMV (or the oracle port) on a bounded
     sample of the same workload: the projections of the first layers, M rows,
-    each with its Q8 quantize. Threads as the reference's bd::ThreadPool(0)
-    (ref/bonsai-decoder/src/cpu_ops.cpp:19-21): every CPU the process may run
-    on, no cap; then the same sample on one thread. budget_s is split 2:1
-    between the two runs."""
+    each with its Q8 quantize, and the output projection. Threads as the
+    reference's bd::ThreadPool(0) (ref/bonsai-decoder/src/cpu_ops.cpp:19-21):
+    every CPU the process may run on, no cap; then the layer sets on one
+    thread. budget_s is split 2:1 between the two runs (plus a sixth for the
+    output projection). `value` is config 5's bytes over the composed token
+    time: 64 x the mean measured layer set + the measured output projection."""
     import numpy as np
     sys.path.insert(0, ORACLE)
     from btf_oracle import Oracle, Ref, have_ref
@@ -775,10 +804,44 @@ def cpu_baseline(S: Setup, step: Step, budget_s=12.0):
 
     gbs, sets, tt = run(allowed, budget_s * 2 / 3)
     gbs1, sets1, tt1 = run(1, budget_s / 3)
+    # config 5 = 64 layer sets + the output projection 5120 -> 248320 (5.7 %
+    # of its bytes): the projection timed too, on every allowed thread, and
+    # the token composed as 64 x the mean measured layer set + it
+    out_t = None
+    if step.with_output and M == 1:
+        codes, scales = S.host_mat("output", step.layers)
+        reps, t_out = 0, 0.0
+        while t_out < max(1.0, budget_s / 6) or reps < 2:
+            t0 = time.perf_counter()
+            O.quantize_rows(xe)
+            tq = time.perf_counter() - t0
+            if R is not None:
+                t, _ = R.emu_gemv_timed(codes, scales, E, qe, de, se, reps=1, threads=allowed)
+            else:
+                t0 = time.perf_counter()
+                O.gemv(codes, scales, E, qe, de, se, nthreads=allowed)
+                t = time.perf_counter() - t0
+            t_out += t + tq
+            reps += 1
+        out_t = t_out / reps
+        del codes, scales
+    layer_b = sum(gemv_bytes(N, K, M) + prep_bytes(K, M) for N, K in ((QKV, E), (E, E), (F, E), (F, E), (E, F)))
+    t_layer = layer_b / (gbs * 1e9)  # mean measured time of one layer set
+    token = None
+    if out_t is not None:
+        t_tok = LAYERS * t_layer + out_t
+        token = {"per_token_s": round(t_tok, 4), "tok_s": round(1.0 / t_tok, 4),
+                 "GBs_over_config5_bytes": round(step.total_bytes / t_tok / 1e9, 3),
+                 "output_projection_s": round(out_t, 4), "layer_set_s": round(t_layer, 5),
+                 "composition": "64 x the mean measured layer set (5 GEMVs with their quantizes) + the measured "
+                                "output projection with its quantize, all on every allowed thread (config 5 on "
+                                "the CPU: the sum of its 321 GEMVs and quantizes, BASELINE section 3)"}
     what = ("reference EmuDecoder::gemv (src/emu_decoder.cpp:143-165) built from the reference sources"
             if kind == "reference" else "oracle port of EmuDecoder::gemv")
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": allowed, "kind": kind,
-            "tok_s_equiv": round(gbs * 1e9 / step.total_bytes, 4) if M == 1 else None,
+    return {"value": round(token["GBs_over_config5_bytes"] if token else gbs, 3), "unit": "GB/s", "cores": allowed,
+            "kind": kind, "config5_token": token,
+            "layer_sets_GBs": round(gbs, 3),
+            "tok_s_equiv": token["tok_s"] if token else (round(gbs * 1e9 / step.total_bytes, 4) if M == 1 else None),
             "value_1_thread": round(gbs1, 3),
             "tok_s_equiv_1_thread": round(gbs1 * 1e9 / step.total_bytes, 4) if M == 1 else None,
             "cpu_model": model, "logical_cpus_allowed": allowed, "logical_cpus_host": logical,
@@ -841,16 +904,33 @@ def write_synth_gguf(path, layers, seed=0, chunk=1 << 26):
 
 
 def run_load(args, hip, torch):
-    """--workload load: GGUF file -> staged upload -> resident T2 layout of
-    every PTQ1_0 matrix (btf_hip_gguf_* + btf_hip_loader_*), from the page
-    cache; `value` = PTQ1_0 bytes read from the file / wall time of the whole
-    upload (open, plan, every upload, finish), median of the timed loads."""
+    """--workload load: the load sub-result as its own line."""
+    layers = args.layers if args.layers != LAYERS else 8
+    r = load_result(hip, torch, layers, args.steps, args.warmup, args.cpu_budget, args.no_cpu)
+    out = {
+        "metric": "PTQ1_0 GGUF load GB/s (file in page cache -> resident T2 layout)", "value": r["GBs"],
+        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": r["ms"],
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
+        "data": "synthetic GGUF (seeded PTQ1_0 bytes) of the 27B shapes",
+        "config": {"workload": r["workload"], "parallelism": "single GPU"},
+        "load": r, "cpu_baseline": r["cpu_baseline"],
+    }
+    print(json.dumps(out), flush=True)
+
+
+def load_result(hip, torch, layers, steps, warmup, cpu_budget, no_cpu):
+    """GGUF file -> staged upload -> resident T2 layout of every PTQ1_0
+    matrix (btf_hip_gguf_* + btf_hip_loader_*), from the page cache: PTQ1_0
+    bytes read from the file / wall time of the whole upload (open, plan,
+    every upload, finish), median of the timed loads; beside it the
+    reference's host repack (btf::repack_rows, src/repack.cpp:16-27, as
+    tools/btf_plan.cpp:72-110 times it) on the same matrices, on every
+    allowed thread."""
     import tempfile
     import numpy as np
     staging = 64 << 20
     tmp = tempfile.mkdtemp(prefix="btf_load_")
     path = os.path.join(tmp, "synth.gguf")
-    layers = args.layers if args.layers != LAYERS else 8
     t0 = time.time()
     src_bytes = write_synth_gguf(path, layers)
     log(f"synthetic GGUF: {layers} layers + output, {os.path.getsize(path) / 1e9:.3f} GB file "
@@ -859,7 +939,7 @@ def run_load(args, hip, torch):
         while f.read(1 << 26):
             pass
     arena, times, plan, phases = None, [], None, []
-    for rep in range(args.warmup + args.steps):
+    for rep in range(warmup + steps):
         t0 = time.perf_counter()
         g = hip.Gguf(path)
         plan = g.plan(staging)
@@ -884,7 +964,7 @@ def run_load(args, hip, torch):
         L.close()
         g.close()
         assert n == plan["source_bytes"] == src_bytes
-        if rep >= args.warmup:
+        if rep >= warmup:
             times.append(dt)
             phases.append((t1 - t0, t2 - t1, dt - (t2 - t0)))
     t = float(np.median(times))
@@ -928,43 +1008,55 @@ def run_load(args, hip, torch):
     e1.close()
     g.close()
     cpu = None
-    if not args.no_cpu:
+    if not no_cpu:
         sys.path.insert(0, ORACLE)
+        from concurrent.futures import ThreadPoolExecutor
         from btf_oracle import Oracle, Ref, have_ref
         kind = "reference" if have_ref() else "port"
         R = Ref() if kind == "reference" else Oracle()
+        model, allowed, logical = cpu_info()
         g = hip.Gguf(path)
-        tm = g.tensor("blk.0.ffn_down.weight")
-        K, N = tm.ne
-        srcm = np.frombuffer(C.string_at(tm.data, tm.bytes), dtype=np.uint8).reshape(N, K // 128 * 28)
-        done, tt = 0, 0.0
-        while tt < min(args.cpu_budget, 6.0):
-            t0 = time.perf_counter()
-            R.repack_rows(srcm, N, K)
-            tt += time.perf_counter() - t0
-            done += srcm.size
+        # every PTQ1_0 matrix of layer 0 and the output projection (the
+        # reference repacks matrix by matrix over a thread pool: row ranges
+        # here, one per thread, the GIL released inside the library)
+        srcs = []
+        for ti in g.tensors:
+            if ti.type == 143 and ti.n_dims == 2 and (ti.name.startswith("blk.0.") or ti.name == "output.weight"):
+                K, N = ti.ne
+                srcs.append((np.frombuffer(C.string_at(ti.data, ti.bytes), dtype=np.uint8).reshape(N, K // 128 * 28),
+                             N, K))
         g.close()
-        cpu = {"value": round(done / tt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
-               "sample": f"host repack of the 5120 x 17408 down matrix ({srcm.size / 1e6:.1f} MB of PTQ1_0), "
-                         f"{done // srcm.size} passes, {tt:.2f} s; "
-                         f"{'reference btf::repack_rows (src/repack.cpp:16-27) built from the reference sources' if kind == 'reference' else 'oracle port of repack_rows'}, one thread"}
+        jobs = []
+        for m, N, K in srcs:
+            step_rows = (N + allowed - 1) // allowed
+            for r0 in range(0, N, step_rows):
+                jobs.append((np.ascontiguousarray(m[r0:r0 + step_rows]), min(step_rows, N - r0), K))
+        nbytes = sum(j[0].size for j in jobs)
+        done, tt, passes = 0, 0.0, 0
+        with ThreadPoolExecutor(max_workers=allowed) as ex:
+            while tt < cpu_budget:
+                t0 = time.perf_counter()
+                list(ex.map(lambda j: R.repack_rows(*j), jobs))
+                tt += time.perf_counter() - t0
+                done += nbytes
+                passes += 1
+        cpu = {"value": round(done / tt / 1e9, 3), "unit": "GB/s", "cores": allowed, "kind": kind,
+               "sample": f"host repack of layer 0's five matrices and the output projection "
+                         f"({nbytes / 1e6:.0f} MB of PTQ1_0), {passes} passes, {tt:.2f} s, row ranges over "
+                         f"{allowed} threads; "
+                         f"{'reference btf::repack_rows (src/repack.cpp:16-27) built from the reference sources' if kind == 'reference' else 'oracle port of repack_rows'}"
+                         f"; the reference's published rate: 2.65 GB/s on 8 vCPUs (README.md:36)",
+               "cpu_model": model}
     os.remove(path)
     os.rmdir(tmp)
-    out = {
-        "metric": "PTQ1_0 GGUF load GB/s (file in page cache -> resident T2 layout)", "value": round(value, 2),
-        "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(t * 1e3, 2),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "u8",
-        "data": "synthetic GGUF (seeded PTQ1_0 bytes) of the 27B shapes",
-        "config": {"workload": f"load {layers} layers x (QKV, o, gate, up, down) + output projection, "
-                               f"{src_bytes} B of PTQ1_0 -> {plan['arena_bytes']} B resident, 2 x 64 MiB staging",
-                   "parallelism": "single GPU"},
-        "stages_gbs": {"host_copy": round(host_gbs, 2), "copy_engine": round(dma_gbs, 2),
-                       "repack_kernel": round(rep_gbs, 1)},
-        "phases_ms": {"open_plan": round(ph[0] * 1e3, 2), "loader_create": round(ph[1] * 1e3, 2),
-                      "uploads": round(ph[2] * 1e3, 2)},
-        "cpu_baseline": cpu,
-    }
-    print(json.dumps(out), flush=True)
+    return {"workload": f"load {layers} layers x (QKV, o, gate, up, down) + output projection, "
+                        f"{src_bytes} B of PTQ1_0 -> {plan['arena_bytes']} B resident, 2 x 64 MiB staging",
+            "GBs": round(value, 2), "ms": round(t * 1e3, 2), "seconds": round(t, 4), "bytes": src_bytes,
+            "stages_gbs": {"host_copy": round(host_gbs, 2), "copy_engine": round(dma_gbs, 2),
+                           "repack_kernel": round(rep_gbs, 1)},
+            "phases_ms": {"open_plan": round(ph[0] * 1e3, 2), "loader_create": round(ph[1] * 1e3, 2),
+                          "uploads": round(ph[2] * 1e3, 2)},
+            "cpu_baseline": cpu}
 
 
 def main():
@@ -1218,8 +1310,12 @@ def main():
                              "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
                              "kernel": "gemv_dot4_kernel (o projection)", "bytes_per_launch": d["bytes"],
                              "avg_launch_us": d["avg_us"]}}
-        subs["config3_batched_m8"] = run_batched_sub(S, 8, 8, args.steps, args.warmup, traffic_tab)
+        for M in (4, 8, 16, 32):
+            subs[f"config3_batched_m{M}"] = run_batched_sub(S, M, 8, args.steps, args.warmup, traffic_tab)
         subs["config4_prefill_m512"] = run_batched_sub(S, 512, 8, max(5, args.steps // 2), 2, traffic_tab)
+        subs["stream_read_ceiling"] = stream_ceiling(S)
+        log(f"stream read ceiling: {subs['stream_read_ceiling']['GBs']} GB/s")
+        subs["load"] = load_result(hip, torch, 8, 3, 1, min(args.cpu_budget, 6.0), args.no_cpu)
 
     out = {
         "metric": METRIC,
@@ -1249,6 +1345,7 @@ def main():
             "parallelism": "single GPU",
         },
         "frac_of_8TBs": round(value / HBM_PEAK_GBS, 4),
+        "frac_of_stream_read": round(value / subs["stream_read_ceiling"]["GBs"], 4) if subs else None,
         "tok_s_equiv": round(1e3 / ms, 2) if args.workload == "sweep" else None,
         "roofline": roof,
         "verified": {"vs_graph_engine_bit_exact": verified} if verified else None,

@@ -119,6 +119,7 @@ _launch_gemv_ptq1_0 = _decl("btf_hip_launch_gemv_ptq1_0",
 _dump = _decl("btf_hip_gemv_i32_dump", [_vp, _i, _i, _i, C.POINTER(_Q8Act), _vp, _vp])
 _set_policy = _decl("btf_hip_gemv_set_policy", [_i])
 _gen = _decl("btf_hip_gen_ptq1_0", [C.c_uint64, C.c_uint64, _i64, _i64, _vp, _vp])
+_stream_read = _decl("btf_hip_stream_read", [_vp, C.c_uint64, C.c_uint32, _vp, _vp])
 _last_error = _decl("btf_hip_last_error", [], C.c_char_p)
 _device_info = _decl("btf_hip_device_info", [_i, C.POINTER(_DeviceInfo)])
 _graph_begin = _decl("btf_hip_graph_begin", [_vp])
@@ -163,7 +164,7 @@ ABI_SYMBOLS = (
     "btf_hip_kernels_init", "btf_hip_gemv_max_nb", "btf_hip_launch_repack", "btf_hip_launch_prep",
     "btf_hip_launch_gemv", "btf_hip_launch_gemv_ex", "btf_hip_launch_gemv_ptq1_0", "btf_hip_launch_embed", "btf_hip_argmax_part_bytes",
     "btf_hip_launch_argmax", "btf_hip_launch_argmax_noalloc", "btf_hip_launch_pos_add", "btf_hip_last_error", "btf_hip_gemv_i32_dump", "btf_hip_gemv_set_policy",
-    "btf_hip_gen_ptq1_0", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
+    "btf_hip_gen_ptq1_0", "btf_hip_stream_read", "btf_hip_device_info", "btf_hip_device_count", "btf_hip_set_device", "btf_hip_malloc",
     "btf_hip_free", "btf_hip_host_alloc_mapped", "btf_hip_host_free", "btf_hip_memcpy_h2d", "btf_hip_memcpy_d2h",
     "btf_hip_memset", "btf_hip_device_synchronize", "btf_hip_stream_create", "btf_hip_stream_destroy",
     "btf_hip_stream_synchronize", "btf_hip_event_create", "btf_hip_event_destroy", "btf_hip_event_record",
@@ -387,6 +388,12 @@ def gemv_set_policy(mfma_min_m: int) -> int:
 def gen_ptq1_0(seed: int, mat: int, first_block: int, nblocks: int, dst, stream=None) -> None:
     """Seeded synthetic PTQ1_0 blocks on the device (benchmark weights)."""
     _check(_gen(seed, mat, first_block, nblocks, _addr(dst), _stream(stream)))
+
+
+def stream_read(src, nbytes: int, sink, stream=None, never: int = 0x9E3779B9) -> None:
+    """btf_hip_stream_read: a plain streaming read of nbytes at src (the
+    practical HBM read ceiling); *sink is written only if the fold equals `never`."""
+    _check(_stream_read(_addr(src), nbytes, never, _addr(sink), _stream(stream)))
 
 
 @dataclass

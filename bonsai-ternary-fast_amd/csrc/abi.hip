@@ -314,6 +314,15 @@ int btf_hip_gemv_set_policy(int mfma_min_m) {
   return prev;
 }
 
+int btf_hip_stream_read(const void* src, uint64_t bytes, uint32_t never, uint32_t* sink, btf_stream_t stream) {
+  if (bytes == 0) return BTF_OK;
+  if (!src || !sink || !aligned(src, 16) || bytes % 16)
+    return fail(BTF_ERR_ARGS, "stream_read: src 16-byte aligned, bytes a multiple of 16, non-null sink");
+  const DevState* ds = current_state();
+  if (!ds) return BTF_ERR_NOT_INIT;
+  return stream_read(src, bytes, never, sink, static_cast<hipStream_t>(stream), *ds);
+}
+
 int btf_hip_gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst,
                        btf_stream_t stream) {
   if (nblocks <= 0) return BTF_OK;

@@ -190,6 +190,7 @@ int step_guards(StepProgram* P, int* guards);
 int step_audit(const btf_step_vec* vecs, int nvec, const btf_step_op* ops, int nops, int G, btf_step_audit* res);  // host only
 void step_destroy(StepProgram* P);
 
+int stream_read(const void* src, uint64_t bytes, uint32_t never, uint32_t* sink, hipStream_t st, const DevState& ds);
 int gen_ptq1_0(uint64_t seed, uint64_t mat, int64_t first_block, int64_t nblocks, uint8_t* dst, hipStream_t st,
                const DevState& ds);
 int embed(const uint8_t* codes, const uint16_t* scales, const int* d_tok, int M, int E, int block, const float* signs,

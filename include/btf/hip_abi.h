@@ -182,6 +182,13 @@ int btf_hip_launch_gemv_ptq1_0(const btf_gemv_seg* segs, int nseg, int K, int M,
  * Process-global; for tests and benchmarks. Returns the previous value. */
 int btf_hip_gemv_set_policy(int mfma_min_m);
 
+/* Measurement hook, no reference counterpart: a plain streaming read of
+ * `bytes` of device memory at src (16-byte words, non-temporal loads as the
+ * GEMV kernels read their weights), the practical HBM read ceiling the GEMV
+ * figures are read against. The words are folded and *sink is written only
+ * if the fold equals `never`. src 16-byte aligned, bytes % 16 == 0. */
+int btf_hip_stream_read(const void* src, uint64_t bytes, uint32_t never, uint32_t* sink, btf_stream_t stream);
+
 /* Seeded synthetic PTQ1_0 blocks (the benchmark's weight generator): blocks
  * [first_block, first_block + nblocks) of matrix `mat`, trits i.i.d. with
  * P(-1,0,+1) = (0.3,0.4,0.3) and fp16 scales RNE(U[0.01,0.05]). dst is
