@@ -1307,7 +1307,9 @@ def main():
                             "past the 256 MB MALL), Q8 input quantized by its own launch",
                 "avg_us": d["avg_us"], "bytes_per_launch": d["bytes"], "GBs": d["GBs"],
                 "roofline": {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                             "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": None,
+                             "frac": round(d["GBs"] / HBM_PEAK_GBS, 4),
+                             "traffic": traffic_tab.get("config1/o", {}).get("hbm_bytes"),
+                             "traffic_source": traffic_tab.get("config1/o", {}).get("source"),
                              "kernel": "gemv_dot4_kernel (o projection)", "bytes_per_launch": d["bytes"],
                              "avg_launch_us": d["avg_us"]}}
         for M in (4, 8, 16, 32):
