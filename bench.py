@@ -581,7 +581,7 @@ def gemm_roofline(step, per, traffic_tab=None, workload="batched"):
     d = per[dom]
     if step.M <= 32:
         tr = (traffic_tab or {}).get(f"batched{step.M}/{dom}")
-        kern = "gemv_dot4_kernel" if step.M < 3 else "gemm_ks_kernel"
+        kern = "gemv_dot4_kernel" if step.M < 3 else "gemm_kp_kernel" if step.M <= 16 else "gemm_ks_kernel"
         return dom, {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
                      "traffic_source": tr["source"] if tr else None, "kernel": f"{dom} GEMM ({kern})",

@@ -1,8 +1,13 @@
 // gemm_mfma.hip -- ternary GEMM on T2 codes with int8 MFMA (gfx950), for
 // batched decode and prefill. Same contract as the reference's gemv_kernel
 // (src/cuda/kernels.cu:238-334) for M activation rows. Kernels:
-//   gemm_ks_kernel   up to 32 rows (batched decode): 16 weight rows per
-//                    workgroup, K split over its waves;
+//   gemm_kp_kernel   up to 16 rows (batched decode): 16 weight rows per
+//                    workgroup, K split over its waves, two 32-column
+//                    sub-blocks of 8 rows per 16x16x64 MFMA, an LDS-direct
+//                    ring per wave;
+//   gemm_ks_kernel   17 to 32 rows (and up to 16 when d or s are not 16-byte
+//                    aligned): the same workgroup, one sub-block per
+//                    16x16x32 MFMA, staged through registers;
 //   gemm_pf2_kernel  more rows (prefill): 64 weight rows x 64 or 128
 //                    activation rows, fed by an LDS-direct ring;
 //   gemm_pf_kernel   the same tile staged through registers (activation
@@ -63,6 +68,34 @@ struct MfmaArgs {
   float* od;
   int32_t* os;
 };
+
+// ---- LDS-direct loads (the packed K-split tile and the prefill tile) ----
+// vmcnt(N) alone (expcnt, lgkmcnt not waited on).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
+// One wave-wide load into LDS: lane l's 16 bytes from g land at LDS byte
+// address lds + 16 l; a 2-byte load fills the low half of the 4-byte slot at
+// lds + 4 l (sub-dword loads keep 4-byte lane slots). Issued as inline assembly so that the compiler's
+// wait insertion does not order every later LDS read behind it; the kernel
+// waits with wait_vm itself. The LDS base is an input bound to M0 (the
+// "{m0}" constraint): the compiler writes M0 itself and knows what it holds;
+// the statement adds the one wait state an LDS-direct load needs after an
+// SALU write of M0.
+__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
+__device__ __forceinline__ void lds_dma4(const void* g, uint32_t lds) {
+  asm volatile("s_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory");
+}
 
 // K-split tile for batched decode (up to 32 activation rows): a workgroup of
 // NW waves owns 16 weight rows (swiglu: 16 gate rows and the same 16 up rows)
@@ -350,6 +383,323 @@ void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st)
     by_mode_ks<4, MT, DUMP, TR>(mode, a, grid, st);
 }
 
+// Packed K-split tile for batched decode (up to 16 activation rows). The
+// workgroup and the K split are gemm_ks_kernel's (16 * TR weight rows, for
+// swiglu with their up rows; wave w walks its contiguous 1/NW of the
+// 128-column blocks), but one v_mfma_i32_16x16x64_i8 covers two 32-column
+// sub-blocks of 8 activation rows: A rows 0-7 hold q of rows 8mg .. 8mg + 7
+// over sub-block 2P (k 0-31: lane groups 0 and 1) and A rows 8-15 the same
+// rows over sub-block 2P + 1 (k 32-63: lane groups 2 and 3), zero elsewhere,
+// so every MFMA output is a real I (no padding rows). The codes enter as
+// stored (0 / 1 / 2; a lane group's 16 columns are one code word, whose four
+// 2-bit fields are its four int8 words after shift and mask) and the
+// accumulator starts at -s, so the MFMA gives I = sum (code - 1) * q exactly.
+// Lane groups 0-1 hold the even sub-blocks and 2-3 the odd ones of the same
+// 16 x 8 outputs; each keeps its own sums (blk = d * I over the block's two
+// sub-blocks of its parity, acc += scale * blk per block), and per output
+//     y = sum over waves w, in order, of (accE_w + accO_w).
+// Each wave streams its blocks two at a time through a private S-stage ring
+// of LDS-direct loads (no registers held by loads in flight): each code load
+// reads 64 contiguous bytes (two blocks) of each of 16 rows, a pattern that
+// streams near the HBM rate where 32 bytes of 32 rows per load did not.
+// Stages past the wave's range reload its last block (L2 hits, never read
+// back) to keep the per-stage load count. Stage layout (bytes): codes
+// [R][4 x 16 B] with chunk c of row n at slot c ^ ((n >> 2) & 3) (the 64
+// lanes' words then fall in 64 banks), scales [2][R] in 4-byte slots, q
+// [2][BQ][8 x 16 B] with chunk c of row r at slot c ^ (r & 7), then 256 zero
+// bytes (the A lanes that carry no data read one 16-byte chunk of them, on
+// banks that the data lanes of the same pass leave free), d
+// [MG][2][4][8] and s [MG][2][4][8] (row group, block, sub-block, row; s
+// negated in place once the stage has landed, so it seeds the accumulator as
+// it is).
+template <int NW, int MG, int S, int MODE, bool DUMP, int TR = 1>
+__global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
+  constexpr int G1 = MODE == BTF_GEMV_SWIGLU ? 2 : 1;
+  constexpr int G = G1 * TR;  // 16-row groups: tile t, matrix g1 at t * G1 + g1
+  constexpr int R = 16 * G;   // staged weight rows per wave
+  constexpr int BQ = 8 * MG;  // activation rows
+  constexpr int CB = R * 64, SB = 2 * R * 4, QB = 2 * BQ * 128 + 256, DB = BQ * 32;
+  constexpr int STG = CB + SB + QB + 2 * DB;
+  constexpr int NCI = R / 16;                   // code loads per stage (16 rows x 64 B each)
+  constexpr int L = NCI + 2 + 2 * MG + 2 * MG;  // loads per stage and wave: codes, scales x 2, q x 2 x MG, d, s
+  static_assert(STG % 16 == 0 && S >= 2 && L * (S - 2) < 64 && R <= 64, "stage layout");
+  constexpr int RING = NW * S * STG, RED = NW * G * 2 * 16 * BQ * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t ring[RING > RED ? RING : RED];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: ring base and K range
+  const int li = lane & 15;
+  const int t = lane >> 4;
+
+  const int bx = blockIdx.x;
+  const int seg = (bx >= a.tile_start[1]) + (bx >= a.tile_start[2]);
+  const uint8_t* codes = seg == 0 ? a.codes[0] : seg == 1 ? a.codes[1] : a.codes[2];
+  const uint16_t* scales = seg == 0 ? a.scales[0] : seg == 1 ? a.scales[1] : a.scales[2];
+  float* y = seg == 0 ? a.y[0] : seg == 1 ? a.y[1] : a.y[2];
+  const int N = seg == 0 ? a.N[0] : seg == 1 ? a.N[1] : a.N[2];
+  const int ldy = seg == 0 ? a.ldy[0] : seg == 1 ? a.ldy[1] : a.ldy[2];
+  const int tile0 = seg == 0 ? 0 : seg == 1 ? a.tile_start[1] : a.tile_start[2];
+  const int K = a.K;
+  const int rowb = K >> 2, nsc = K >> 7, nsub = a.nsub;
+  const int n0 = (bx - tile0) * 16 * TR;
+  const int mb = blockIdx.y * BQ;
+  const int kw0 = nsc * w / NW, kw1 = nsc * (w + 1) / NW;
+  const int niter = ((nsc + NW - 1) / NW + 1) / 2;  // every wave runs the longest range's stage count
+
+  uint8_t* rw = ring + w * (S * STG);
+  const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)rw;  // LDS byte address
+
+  // ---- this lane's load sources (block offsets added per stage, clamped to the row) ----
+  const uint8_t* csrc[NCI];  // codes: load j -> row 16 j + lane / 4, slot lane % 4
+  int cblk[NCI];             // which of the stage's two blocks that slot holds
+#pragma unroll
+  for (int j = 0; j < NCI; ++j) {
+    const int n = 16 * j + (lane >> 2);
+    const int h = (lane & 3) ^ ((n >> 2) & 3);
+    const int nr = n0 + 16 * ((n >> 4) / G1) + (n & 15);
+    const int nc = nr < N ? nr : N - 1;
+    csrc[j] = ((n >> 4) % G1 ? a.up_codes : codes) + (size_t)nc * rowb + 16 * (h & 1);
+    cblk[j] = h >> 1;
+  }
+  const uint16_t* ssrc;  // scales: lane < R -> row lane
+  {
+    const int n = lane < R ? lane : R - 1;
+    const int nr = n0 + 16 * ((n >> 4) / G1) + (n & 15);
+    const int nc = nr < N ? nr : N - 1;
+    ssrc = ((n >> 4) % G1 ? a.up_scales : scales) + (size_t)nc * nsc;
+  }
+  const int8_t* qsrc[MG];  // q: load (block, mg) -> row 8 mg + lane / 8, slot lane % 8 holds chunk (lane % 8) ^ (lane / 8)
+#pragma unroll
+  for (int mg = 0; mg < MG; ++mg) {
+    const int r = 8 * mg + (lane >> 3);
+    const int m = mb + r < a.nb ? mb + r : a.nb - 1;
+    qsrc[mg] = a.q + (size_t)(a.m0 + m) * K + 16 * ((lane & 7) ^ (lane >> 3));
+  }
+  const float* dsrc[MG];  // d and s: load mg -> slot lane of group mg: [block lane / 32][sub-block][row 8 mg + lane % 8]
+  const int32_t* s_src[MG];
+  const int dblk = lane >> 5;  // which of the stage's two blocks
+#pragma unroll
+  for (int mg = 0; mg < MG; ++mg) {
+    const int r = 8 * mg + (lane & 7);
+    const int m = mb + r < a.nb ? mb + r : a.nb - 1;
+    dsrc[mg] = a.d + (size_t)(a.m0 + m) * nsub + ((lane >> 3) & 3);
+    s_src[mg] = a.s + (size_t)(a.m0 + m) * nsub + ((lane >> 3) & 3);
+  }
+  // the wave's last block (a wave with none: block 0); stages past its range reload it
+  const int klast = kw1 > kw0 ? kw1 - 1 : 0;
+  auto issue = [&](int it) {
+    const int kb = kw0 + 2 * it;
+    const uint32_t st = ring0 + (uint32_t)((it % S) * STG);
+    auto blk_of = [&](int i) { return kb + i < klast ? kb + i : klast; };
+#pragma unroll
+    for (int j = 0; j < NCI; ++j) lds_dma16(csrc[j] + (size_t)blk_of(cblk[j]) * 32, st + 1024 * j);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      if (lane < R) lds_dma2(ssrc + blk_of(i), st + CB + i * R * 4);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) lds_dma16(qsrc[mg] + (size_t)blk_of(i) * 128, st + CB + SB + (i * BQ + 8 * mg) * 128);
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg) {
+      lds_dma4(dsrc[mg] + 4 * blk_of(dblk), st + CB + SB + QB + 256 * mg);
+      lds_dma4(s_src[mg] + 4 * blk_of(dblk), st + CB + SB + QB + DB + 256 * mg);
+    }
+  };
+
+  // the zero bytes after the q rows of every stage (no load writes them)
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+    if (lane < 16) *reinterpret_cast<u32x4*>(rw + s * STG + CB + SB + 2 * BQ * 128 + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int it = 0; it < S - 1; ++it) issue(it);
+
+  // ---- this lane's LDS read offsets within a stage ----
+  const int x = li & 7;
+  const bool holds = (li < 8) == (t < 2);  // A lane with data (else the zero row)
+  int aoff[2][MG][2];  // block i, group mg, pair P (the data-less lanes: the zero bytes, for every block)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+      for (int P = 0; P < 2; ++P)
+        aoff[i][mg][P] = CB + SB + (holds ? (i * BQ + 8 * mg + x) * 128 + 16 * ((4 * P) ^ t ^ x)
+                                          : 2 * BQ * 128 + 16 * ((t & 1) ^ 1));
+  int boff[2][2];  // code word 4P + t of block i of row li (group g adds 1024)
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int P = 0; P < 2; ++P) boff[i][P] = li * 64 + 16 * ((2 * i + P) ^ ((li >> 2) & 3)) + 4 * t;
+  // d / s of output rows 4 (t & 1) .. + 3 of group mg, block i, sub-block 2P + (t >> 1): one 16-byte read
+  const int doff = CB + SB + QB + 4 * (8 * (t >> 1) + 4 * (t & 1));
+
+  float acc[G][MG][4], blk[G][MG][4];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[g][mg][r] = 0.f;
+
+  for (int it = 0; it < niter; ++it) {
+    wait_vm<L * (S - 2)>();  // this wave's loads of stage it have landed
+    issue(it + S - 1);       // into the stage read in iteration it - 1
+    const int kb = kw0 + 2 * it;
+    uint8_t* st = rw + (it % S) * STG;
+    {  // s -> -s, in place (each of the stage's 64 MG values once)
+#pragma unroll
+      for (int mg = 0; mg < MG; ++mg) {
+        int32_t* sp = reinterpret_cast<int32_t*>(st + CB + SB + QB + DB + 256 * mg) + lane;
+        *sp = -*sp;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      if (kb + i >= kw1) break;  // (wave-uniform)
+#pragma unroll
+      for (int P = 0; P < 2; ++P) {
+        v4i A[MG], C[MG];
+        float dv[MG][4];
+#pragma unroll
+        for (int mg = 0; mg < MG; ++mg) {
+          A[mg] = *reinterpret_cast<const v4i*>(st + aoff[i][mg][P]);
+          const int o = doff + 256 * mg + 128 * i + 64 * P;
+          const u32x4 dw = *reinterpret_cast<const u32x4*>(st + o);
+          C[mg] = *reinterpret_cast<const v4i*>(st + o + DB);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dv[mg][r] = __uint_as_float(dw[r]);
+        }
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const uint32_t wd = *reinterpret_cast<const uint32_t*>(st + boff[i][P] + 1024 * g);
+          const v4i B = {(int)(wd & 0x03030303u), (int)((wd >> 2) & 0x03030303u), (int)((wd >> 4) & 0x03030303u),
+                         (int)((wd >> 6) & 0x03030303u)};
+#pragma unroll
+          for (int mg = 0; mg < MG; ++mg) {
+            const v4i I = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mg], B, C[mg], 0, 0, 0);
+            if constexpr (DUMP) {
+              const int n = n0 + 16 * (g / G1) + li;
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int m = mb + 8 * mg + 4 * (t & 1) + r;
+                if (g % G1 == 0 && m < a.nb && n < N)
+                  a.dump[((size_t)(a.m0 + m) * N + n) * nsub + (kb + i) * 4 + 2 * P + (t >> 1)] = I[r];
+              }
+            } else {
+#pragma unroll
+              for (int r = 0; r < 4; ++r)
+                blk[g][mg][r] = P == 0 ? dv[mg][r] * (float)I[r] : fmaf(dv[mg][r], (float)I[r], blk[g][mg][r]);
+            }
+          }
+        }
+      }
+      if constexpr (!DUMP) {
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float sc = h2f(*reinterpret_cast<const uint16_t*>(st + CB + i * R * 4 + 4 * (16 * g + li)));
+#pragma unroll
+          for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[g][mg][r] = fmaf(sc, blk[g][mg][r], acc[g][mg][r]);
+        }
+      }
+    }
+  }
+  wait_vm<0>();  // the trailing loads land before the ring is reused or released
+  if constexpr (DUMP) return;
+
+  // ---- per-parity wave partials -> LDS (over the ring), summed per wave, then in wave order ----
+  __syncthreads();
+  float* red = reinterpret_cast<float*>(ring);  // [NW][G][2][16][BQ]
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int mg = 0; mg < MG; ++mg)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        red[(((w * G + g) * 2 + (t >> 1)) * 16 + li) * BQ + 8 * mg + 4 * (t & 1) + r] = acc[g][mg][r];
+  __syncthreads();
+  // thread idx: output row rr = idx % RT of the tile, activation row mm = idx / RT
+  // (with TR = 2 a half-wave holds the 32 outputs of one activation row: one Q8 block)
+  constexpr int RT = 16 * TR;
+  for (int idx = tid; idx < RT * BQ; idx += 64 * NW) {
+    const int rr = idx & (RT - 1), mm = idx / RT;
+    const int n = n0 + rr, m = mb + mm;
+    const bool live = m < a.nb && n < N;
+    if (TR == 1 && !live) continue;
+    const int gb = (rr >> 4) * G1;  // first group of the row's tile
+    float v[G1];
+#pragma unroll
+    for (int g = 0; g < G1; ++g) {
+      const int base = ((gb + g) * 2 * 16 + (rr & 15)) * BQ + mm;  // wave 0, even parity
+      float sacc = red[base] + red[base + 16 * BQ];
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) {
+        const int o = base + ww * G * 2 * 16 * BQ;
+        sacc = sacc + (red[o] + red[o + 16 * BQ]);
+      }
+      v[g] = sacc;
+    }
+    float* o = &y[(size_t)(a.m0 + m) * ldy + n];
+    float out = 0.f;
+    if (live) {
+      if constexpr (MODE == BTF_GEMV_SWIGLU)
+        out = v[0] / (1.0f + expf(-v[0])) * v[G1 - 1];
+      else if constexpr (MODE == BTF_GEMV_ADD)
+        out = *o + v[0];
+      else
+        out = v[0];
+      *o = out;
+    }
+    if constexpr (TR == 2) {
+      if (a.oq) {  // (uniform) the Q8 block of rows n0 .. n0 + 31 of activation row m
+        float dq;
+        int sq;
+        const int q = q8_half(out, dq, sq);
+        uint32_t wq = (uint32_t)(q & 0xff) << (8 * (rr & 3));
+        wq |= (uint32_t)dpp_i<0xB1>((int)wq);  // quad_perm(1,0,3,2)
+        wq |= (uint32_t)dpp_i<0x4E>((int)wq);  // quad_perm(2,3,0,1)
+        if (live) {
+          const size_t mr = (size_t)(a.m0 + m);
+          if ((rr & 3) == 0) *reinterpret_cast<uint32_t*>(a.oq + mr * N + n) = wq;
+          if (rr == 0) {
+            a.od[mr * (N / 32) + n0 / 32] = dq;
+            a.os[mr * (N / 32) + n0 / 32] = sq;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Two stages per wave (deeper rings measured no faster at M = 4, 8 and 16:
+// their LDS cost resident workgroups).
+template <int NW, int MG, bool DUMP, int TR>
+void by_mode_kp(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  constexpr int S = 2;
+  if (mode == BTF_GEMV_STORE)
+    hipLaunchKernelGGL((gemm_kp_kernel<NW, MG, S, BTF_GEMV_STORE, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
+  else if (mode == BTF_GEMV_ADD)
+    hipLaunchKernelGGL((gemm_kp_kernel<NW, MG, S, BTF_GEMV_ADD, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
+  else
+    hipLaunchKernelGGL((gemm_kp_kernel<NW, MG, S, BTF_GEMV_SWIGLU, DUMP, TR>), grid, dim3(64 * NW), 0, st, a);
+}
+
+// Waves per workgroup (the K split, so the outputs' summation order depends
+// on it; every caller of a shape gets the same): gate+up 2, K >= 8192 8,
+// else 4 (measured best of 2 / 4 / 8 at M = 4, 8, 16 on the 27B shapes).
+template <int MG, bool DUMP, int TR = 1>
+void by_waves_kp(int K, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  if (mode == BTF_GEMV_SWIGLU)
+    by_mode_kp<2, MG, DUMP, TR>(mode, a, grid, st);
+  else if (K >= 8192)
+    by_mode_kp<8, MG, DUMP, TR>(mode, a, grid, st);
+  else
+    by_mode_kp<4, MG, DUMP, TR>(mode, a, grid, st);
+}
+
 // Prefill tile (more than 32 activation rows): a workgroup owns 64 staged
 // weight rows (swiglu: 32 gate rows and the same 32 up rows) and BM = 32 * MW
 // activation rows; wave (wn, wm) = (w & 1, w >> 1) computes 32 staged rows x
@@ -596,30 +946,6 @@ void by_mode_pf(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
     hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_ADD>), grid, dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL((gemm_pf_kernel<MW, KB, BTF_GEMV_SWIGLU>), grid, dim3(256), 0, st, a);
-}
-
-// ---- LDS-direct prefill tile ----
-// vmcnt(N) alone (expcnt, lgkmcnt not waited on).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
-}
-// One wave-wide load into LDS: lane l's 16 bytes from g land at LDS byte
-// address lds + 16 l; a 2-byte load fills the low half of the 4-byte slot at
-// lds + 4 l (sub-dword loads keep 4-byte lane slots). Issued as inline assembly so that the compiler's
-// wait insertion does not order every later LDS read behind it; the kernel
-// waits with wait_vm itself. The LDS base is an input bound to M0 (the
-// "{m0}" constraint): the compiler writes M0 itself and knows what it holds;
-// the statement adds the one wait state an LDS-direct load needs after an
-// SALU write of M0.
-__device__ __forceinline__ void lds_dma16(const void* g, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
-}
-__device__ __forceinline__ void lds_dma2(const void* g, uint32_t lds) {
-  asm volatile("s_nop 0\n\tglobal_load_lds_ushort %0, off" : : "v"(g), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
 }
 
 // The prefill tile of gemm_pf_kernel (64 staged weight rows x BM = 32 * MW
@@ -887,6 +1213,22 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   const dim3 grid(tiles, (nb + BM - 1) / BM);
   const bool dmp = dump != nullptr;
   if (ks) {
+    // up to 16 rows with d and s 16-byte aligned (the LDS-direct loads of the
+    // packed tile read them in 16-byte pieces): the packed tile
+    if (nb <= 16 && ((reinterpret_cast<uintptr_t>(act.d) | reinterpret_cast<uintptr_t>(act.s)) & 15) == 0) {
+      const dim3 gk(tiles, 1);
+      if (qout) {
+        if (nb <= 8)
+          by_waves_kp<1, false, 2>(K, mode, a, gk, st);
+        else
+          by_waves_kp<2, false, 2>(K, mode, a, gk, st);
+      } else if (nb <= 8) {
+        dmp ? by_waves_kp<1, true>(K, mode, a, gk, st) : by_waves_kp<1, false>(K, mode, a, gk, st);
+      } else {
+        dmp ? by_waves_kp<2, true>(K, mode, a, gk, st) : by_waves_kp<2, false>(K, mode, a, gk, st);
+      }
+      return launch_status("gemm_kp_kernel");
+    }
     // 8 waves split K for one activation tile (measured: down 29.6 -> 25.2 us and
     // QKV 11.0 -> 10.1 us at M = 8), except gate+up at K = 5120 (27 -> 31 us);
     // with two activation tiles 8 waves were slower on every shape

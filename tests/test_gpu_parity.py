@@ -394,11 +394,13 @@ def test_gemm_batched_and_prefill(hip, oracle, M):
 
 @pytest.mark.parametrize("K,M", [(128, 3), (384, 17), (1152, 5), (3200, 32), (17536, 9)])
 def test_gemm_k_split_tile_edges(hip, oracle, K, M):
-    """Batches of 3..32 rows run on the K-split 16-row tile (each wave a
-    quarter of the 128-column blocks): block counts that do not split evenly
-    (1 block: three waves idle; 3, 9, 25, 137 blocks), one and two 16-row
-    activation tiles with dead rows, 16-row weight tiles with dead rows
-    (N = 37, 9), and the three modes, against the emulator GEMV."""
+    """Batches of 3..32 rows run on the K-split 16-row tiles (each wave a
+    contiguous share of the 128-column blocks: the packed tile up to 16 rows,
+    two blocks per ring stage, the register-staged tile above): block counts
+    that do not split evenly (1 block: the other waves idle; 3, 9, 25, 137
+    blocks: odd shares), one and two groups of activation rows with dead rows,
+    16-row weight tiles with dead rows (N = 37, 9), and the three modes,
+    against the emulator GEMV."""
     rng = np.random.default_rng(K + 1000 * M)
     _, q, d, s = random_act(oracle, rng, M, K, 3.0)
     act = q8_dev(q, d, s, hip)
@@ -506,6 +508,34 @@ def test_gemm_prefill_unaligned_scales(hip, oracle):
         act = hip.Q8Act(dev(q), dptr, dev(s))
         hip.launch_gemv([hip.GemvSeg(dev(codes), dev(scales), N, y, N)], K, M, act, hip.GemvMode.kStore, stream())
         assert_close_1e3(host(y), ref, "prefill d alignment")
+
+
+@pytest.mark.parametrize("M", [5, 8, 13])
+def test_gemm_batched_unaligned_scales(hip, oracle, M):
+    """Up to 16 rows run on the packed tile, whose LDS-direct ring loads d and
+    s in 16-byte pieces; d or s at an 8-byte (not 16-byte) aligned address
+    take the register-staged K-split tile. Every combination against the
+    emulator GEMV (swiglu too), and I of the misaligned case bit-exact."""
+    K, N = 1152, 45  # 9 blocks: the waves' ranges are odd and uneven
+    rng = np.random.default_rng(43 + M)
+    _, q, d, s = random_act(oracle, rng, M, K, 3.0)
+    g, gs = random_mat(oracle, rng, N, K)
+    u, us = random_mat(oracle, rng, N, K)
+    ref = oracle.swiglu(oracle.gemv(g, gs, K, q, d, s), oracle.gemv(u, us, K, q, d, s))
+    torch = _torch()
+    dbuf, sbuf = zeros(d.size + 2, torch.float32), zeros(s.size + 2, torch.int32)
+    dbuf[2:] = dev(d.reshape(-1))
+    sbuf[2:] = dev(s.reshape(-1))
+    G = hip.GemvMode
+    for dptr, sptr in ((dev(d), dev(s)), (dbuf.data_ptr() + 8, dev(s)), (dev(d), sbuf.data_ptr() + 8)):
+        act = hip.Q8Act(dev(q), dptr, sptr)
+        y = zeros((M, N), torch.float32)
+        hip.launch_gemv([hip.GemvSeg(dev(g), dev(gs), N, y, N), hip.GemvSeg(dev(u), dev(us), N, None, 0)], K, M, act,
+                        G.kSwiglu, stream())
+        assert_close_1e3(host(y), ref, f"M={M} swiglu, d/s alignment")
+        out = zeros((M, N, K // 32), torch.int32)
+        hip.gemv_i32_dump(dev(g), N, K, M, act, out, stream())
+        assert np.array_equal(host(out), oracle.gemv_i32(g, K, q, s)), f"M={M} I"
 
 
 def test_prep_then_gemv_end_to_end(hip, oracle):
