@@ -409,9 +409,8 @@ void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st)
 // [2][BQ][8 x 16 B] with chunk c of row r at slot c ^ (r & 7), then 256 zero
 // bytes (the A lanes that carry no data read one 16-byte chunk of them, on
 // banks that the data lanes of the same pass leave free), d
-// [MG][2][4][8] and s [MG][2][4][8] (row group, block, sub-block, row; s
-// negated in place once the stage has landed, so it seeds the accumulator as
-// it is).
+// [MG][2][4][8] and s [MG][2][4][8] (row group, block, sub-block, row: a
+// lane's four rows are one 16-byte read).
 template <int NW, int MG, int S, int MODE, bool DUMP, int TR = 1>
 __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
   constexpr int G1 = MODE == BTF_GEMV_SWIGLU ? 2 : 1;
@@ -535,7 +534,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
   // d / s of output rows 4 (t & 1) .. + 3 of group mg, block i, sub-block 2P + (t >> 1): one 16-byte read
   const int doff = CB + SB + QB + 4 * (8 * (t >> 1) + 4 * (t & 1));
 
-  float acc[G][MG][4], blk[G][MG][4];
+  float acc[G][MG][4];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
@@ -547,62 +546,76 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
     wait_vm<L * (S - 2)>();  // this wave's loads of stage it have landed
     issue(it + S - 1);       // into the stage read in iteration it - 1
     const int kb = kw0 + 2 * it;
-    uint8_t* st = rw + (it % S) * STG;
-    {  // s -> -s, in place (each of the stage's 64 MG values once)
-#pragma unroll
-      for (int mg = 0; mg < MG; ++mg) {
-        int32_t* sp = reinterpret_cast<int32_t*>(st + CB + SB + QB + DB + 256 * mg) + lane;
-        *sp = -*sp;
-      }
-    }
+    if (kb >= kw1) continue;        // (wave-uniform; later iterations only wait and issue)
+    const bool two = kb + 1 < kw1;  // (wave-uniform) the stage's second block is in the wave's range
+    const uint8_t* st = rw + (it % S) * STG;
+    // Per block: every LDS read first, then every MFMA into its own
+    // registers, then the scaling, so that LDS and MFMA latencies overlap
+    // instead of each product waiting for its own operands. A second block
+    // past the wave's range is multiplied on its (valid) staged data but not
+    // accumulated.
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      if (kb + i >= kw1) break;  // (wave-uniform)
+      v4i A[2][MG], C[2][MG];
+      u32x4 D[2][MG];
+      uint32_t W[2][G];
+      uint16_t SC[G];
 #pragma unroll
       for (int P = 0; P < 2; ++P) {
-        v4i A[MG], C[MG];
-        float dv[MG][4];
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg) {
-          A[mg] = *reinterpret_cast<const v4i*>(st + aoff[i][mg][P]);
+          A[P][mg] = *reinterpret_cast<const v4i*>(st + aoff[i][mg][P]);
           const int o = doff + 256 * mg + 128 * i + 64 * P;
-          const u32x4 dw = *reinterpret_cast<const u32x4*>(st + o);
-          C[mg] = *reinterpret_cast<const v4i*>(st + o + DB);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) dv[mg][r] = __uint_as_float(dw[r]);
+          D[P][mg] = *reinterpret_cast<const u32x4*>(st + o);
+          C[P][mg] = *reinterpret_cast<const v4i*>(st + o + DB);
         }
 #pragma unroll
+        for (int g = 0; g < G; ++g) W[P][g] = *reinterpret_cast<const uint32_t*>(st + boff[i][P] + 1024 * g);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) SC[g] = *reinterpret_cast<const uint16_t*>(st + CB + i * R * 4 + 4 * (16 * g + li));
+      v4i I[2][G][MG];
+#pragma unroll
+      for (int P = 0; P < 2; ++P) {
+#pragma unroll
+        for (int mg = 0; mg < MG; ++mg) C[P][mg] = -C[P][mg];  // the accumulator starts at -s
+#pragma unroll
         for (int g = 0; g < G; ++g) {
-          const uint32_t wd = *reinterpret_cast<const uint32_t*>(st + boff[i][P] + 1024 * g);
+          const uint32_t wd = W[P][g];
           const v4i B = {(int)(wd & 0x03030303u), (int)((wd >> 2) & 0x03030303u), (int)((wd >> 4) & 0x03030303u),
                          (int)((wd >> 6) & 0x03030303u)};
 #pragma unroll
-          for (int mg = 0; mg < MG; ++mg) {
-            const v4i I = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[mg], B, C[mg], 0, 0, 0);
-            if constexpr (DUMP) {
-              const int n = n0 + 16 * (g / G1) + li;
+          for (int mg = 0; mg < MG; ++mg) I[P][g][mg] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[P][mg], B, C[P][mg], 0, 0, 0);
+        }
+      }
+      if (i == 1 && !two) break;  // (wave-uniform)
+      if constexpr (DUMP) {  // the exact I of every (row, output, sub-block)
+#pragma unroll
+        for (int P = 0; P < 2; ++P)
+#pragma unroll
+          for (int g = 0; g < G; g += G1) {
+            const int n = n0 + 16 * (g / G1) + li;
+#pragma unroll
+            for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int m = mb + 8 * mg + 4 * (t & 1) + r;
-                if (g % G1 == 0 && m < a.nb && n < N)
-                  a.dump[((size_t)(a.m0 + m) * N + n) * nsub + (kb + i) * 4 + 2 * P + (t >> 1)] = I[r];
+                if (m < a.nb && n < N)
+                  a.dump[((size_t)(a.m0 + m) * N + n) * nsub + (kb + i) * 4 + 2 * P + (t >> 1)] = I[P][g][mg][r];
               }
-            } else {
-#pragma unroll
-              for (int r = 0; r < 4; ++r)
-                blk[g][mg][r] = P == 0 ? dv[mg][r] * (float)I[r] : fmaf(dv[mg][r], (float)I[r], blk[g][mg][r]);
-            }
           }
-        }
-      }
-      if constexpr (!DUMP) {
+      } else {
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-          const float sc = h2f(*reinterpret_cast<const uint16_t*>(st + CB + i * R * 4 + 4 * (16 * g + li)));
+          const float sc = h2f(SC[g]);
 #pragma unroll
           for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) acc[g][mg][r] = fmaf(sc, blk[g][mg][r], acc[g][mg][r]);
+            for (int r = 0; r < 4; ++r) {
+              const float b0 = __uint_as_float(D[0][mg][r]) * (float)I[0][g][mg][r];
+              const float b1 = fmaf(__uint_as_float(D[1][mg][r]), (float)I[1][g][mg][r], b0);
+              acc[g][mg][r] = fmaf(sc, b1, acc[g][mg][r]);
+            }
         }
       }
     }
@@ -676,6 +689,9 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
 
 // Two stages per wave (deeper rings measured no faster at M = 4, 8 and 16:
 // their LDS cost resident workgroups).
+// Two stages per wave (deeper rings measured no faster at M = 4, 8 and 16:
+// their LDS cost resident workgroups, and one wave per gate+up workgroup with
+// 2 to 8 stages took the same time for every depth).
 template <int NW, int MG, bool DUMP, int TR>
 void by_mode_kp(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
   constexpr int S = 2;
