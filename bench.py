@@ -574,13 +574,14 @@ def kind_timings(step, layers, steps, fused=False, b3=False):
     return per
 
 
-def gemm_roofline(step, per, traffic_tab=None, workload="batched"):
+def gemm_roofline(step, per, traffic_tab=None, fused=False):
     """The dominant GEMV/GEMM kind of a batched step and its roofline (HBM
-    below 33 rows, int8 MFMA above)."""
+    below 33 rows, int8 MFMA above); the traffic of the engine's own
+    instance (the Q8-output kernels for the fused engine) when profiled."""
     dom = max(per, key=lambda k: per[k]["avg_us"] * per[k]["launches_per_step"])
     d = per[dom]
     if step.M <= 32:
-        tr = (traffic_tab or {}).get(f"batched{step.M}/{dom}")
+        tr = (traffic_tab or {}).get(f"batched{step.M}{'_fused' if fused else ''}/{dom}")
         kern = "gemv_dot4_kernel" if step.M < 3 else "gemm_kp_kernel" if step.M <= 16 else "gemm_ks_kernel"
         return dom, {"bound": "hbm", "achieved": d["GBs"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(d["GBs"] / HBM_PEAK_GBS, 4), "traffic": tr["hbm_bytes"] if tr else None,
@@ -618,7 +619,7 @@ def run_batched_sub(S: Setup, M, layers, steps, warmup, traffic_tab):
     best = min(ems, key=ems.get)
     ms = ems[best]
     per = kind_timings(step, layers, steps, fused=best == "fused")
-    dom, roof = gemm_roofline(step, per, traffic_tab if best == "graph" else None)
+    dom, roof = gemm_roofline(step, per, traffic_tab, fused=best == "fused")
     log(f"M={M}: {ms:.4f} ms per {layers}-layer step ({best}; " +
         ", ".join(f"{k} {v:.4f}" for k, v in ems.items()) + f"); dominant {dom} {per[dom]['avg_us']} us, "
         f"{roof['achieved']} {roof['unit']} ({100 * roof['frac']:.1f} %)")
@@ -1291,7 +1292,7 @@ def main():
                 "kernel": f"{dom} GEMV (gemv_dot4_kernel{', quantizes fused in' if fk else ''})",
                 "bytes_per_launch": d["bytes"], "avg_launch_us": d["avg_us"]}
     else:
-        _, roof = gemm_roofline(step, per, traffic_tab if not args.mfma_min_m and engine == "graph" else {})
+        _, roof = gemm_roofline(step, per, traffic_tab if not args.mfma_min_m else {}, fused=engine == "chain")
 
     # Sub-results of the default run, each with its own roofline: the whole
     # decode step in one launch; config 1 (the 5120 -> 5120 GEMV, 64 distinct
