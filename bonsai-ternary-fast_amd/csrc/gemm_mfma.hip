@@ -972,8 +972,10 @@ void by_mode_pf(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
 // {-1, 0, +1} with one byte permute per word, so the MFMA yields
 // I = sum q * w directly (accumulator 0) and s is not read. Stage layout:
 // q [BM][128 B] with the 16-byte chunk c of row r at slot c ^ (r & 7) (the A
-// fragments of 16 rows fall in 8 bank groups), codes [64][32 B], d [BM][4],
-// scales [64] in 4-byte slots. Same sums, in the same order, as gemm_pf_kernel.
+// fragments of 16 rows fall in 8 bank groups), codes [64][2 x 16 B] with the
+// halves of row r swapped when bit 3 of r is set (rows r and r + 8 of a
+// fragment read then fall in different banks), d [BM][4], scales [64] in
+// 4-byte slots. Same sums, in the same order, as gemm_pf_kernel.
 template <int MW, int S, int MODE, bool DUMP = false>
 __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
   constexpr int BM = 32 * MW;
@@ -1016,14 +1018,15 @@ __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
     const int m = mb + r < a.nb ? mb + r : a.nb - 1;
     qsrc[i] = a.q + (size_t)(a.m0 + m) * K + 16 * c;
   }
-  // codes (waves 0, 1): slot P = w * 64 + lane -> staged row P / 2, half P % 2
+  // codes (waves 0, 1): slot P = w * 64 + lane -> staged row P / 2, slot P % 2
+  // holding half (P % 2) ^ (bit 3 of the row)
   const uint8_t* csrc;
   {
     const int P = (w & 1) * 64 + lane;
     const int r = P >> 1;
     const int nr = n0 + (SW ? (r & 31) : r);
     const int nc = nr < N ? nr : N - 1;
-    csrc = (SW && r >= 32 ? a.up_codes : codes) + (size_t)nc * rowb + 16 * (P & 1);
+    csrc = (SW && r >= 32 ? a.up_codes : codes) + (size_t)nc * rowb + 16 * ((P & 1) ^ ((r >> 3) & 1));
   }
   // d (waves 2, 3): row (w - 2) * 64 + lane; scales (wave 3): staged row lane
   const float* dsrc;
@@ -1085,7 +1088,9 @@ __global__ void __launch_bounds__(256) gemm_pf2_kernel(MfmaArgs a) {
       long bfrag[2];
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
-        const uint32_t word = *reinterpret_cast<const uint32_t*>(cst + (srow[j] + li) * 32 + 4 * (2 * sb + (t >> 1)));
+        const int wi = 2 * sb + (t >> 1);  // word of the staged row (half wi / 4, stored swapped for rows 8-15 of 16)
+        const uint32_t word =
+            *reinterpret_cast<const uint32_t*>(cst + (srow[j] + li) * 32 + 16 * ((wi >> 2) ^ (li >> 3)) + 4 * (wi & 3));
         const int sh = 4 * (t & 1);
         const uint32_t lo = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> sh) & 0x03030303u);
         const uint32_t hi = __builtin_amdgcn_perm(0u, 0x000100FFu, (word >> (sh + 2)) & 0x03030303u);
