@@ -383,6 +383,10 @@ void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st)
     by_mode_ks<4, MT, DUMP, TR>(mode, a, grid, st);
 }
 
+// The longest wave range (128-column blocks) the packed tile's preloads hold:
+// the host picks the waves per workgroup so that ceil(nsc / NW) fits.
+__host__ __device__ constexpr int kp_max_blocks(int nw) { return nw == 4 ? 16 : 20; }
+
 // Packed K-split tile for batched decode (up to 16 activation rows). The
 // workgroup and the K split are gemm_ks_kernel's (16 * TR weight rows, for
 // swiglu with their up rows; wave w walks its contiguous 1/NW of the
@@ -400,12 +404,15 @@ void by_waves_ks(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st)
 //     y = sum over waves w, in order, of (accE_w + accO_w).
 // Each wave streams its blocks two at a time through a private S-stage ring
 // of LDS-direct loads (no registers held by loads in flight): each code load
-// reads 64 contiguous bytes (two blocks) of each of 16 rows, a pattern that
-// streams near the HBM rate where 32 bytes of 32 rows per load did not.
-// Stages past the wave's range reload its last block (L2 hits, never read
-// back) to keep the per-stage load count. Stage layout (bytes): codes
+// reads 64 contiguous bytes (two blocks) of each of 16 rows. With one row
+// group (MG = 1) the weight scales of the wave's whole range are loaded once,
+// before the first stage, into [R][SR] 4-byte slots after the ring: a stage
+// of 2 blocks then carries no scale loads (their HBM lines, apart from the
+// code rows, cost ~2.5 us of gate+up at M = 8 when every stage fetched its
+// own). Stages past the wave's range reload its last block (L2 hits, never
+// read back) to keep the per-stage load count. Stage layout (bytes): codes
 // [R][4 x 16 B] with chunk c of row n at slot c ^ ((n >> 2) & 3) (the 64
-// lanes' words then fall in 64 banks), scales [2][R] in 4-byte slots, q
+// lanes' words then fall in 64 banks), scales [2][R] in 4-byte slots (MG = 2), q
 // [2][BQ][8 x 16 B] with chunk c of row r at slot c ^ (r & 7), then 256 zero
 // bytes (the A lanes that carry no data read one 16-byte chunk of them, on
 // banks that the data lanes of the same pass leave free), d
@@ -417,12 +424,20 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
   constexpr int G = G1 * TR;  // 16-row groups: tile t, matrix g1 at t * G1 + g1
   constexpr int R = 16 * G;   // staged weight rows per wave
   constexpr int BQ = 8 * MG;  // activation rows
-  constexpr int CB = R * 64, SB = 2 * R * 4, QB = 2 * BQ * 128 + 256, DB = BQ * 32;
-  constexpr int STG = CB + SB + QB + 2 * DB;
-  constexpr int NCI = R / 16;                   // code loads per stage (16 rows x 64 B each)
-  constexpr int L = NCI + 2 + 2 * MG + 2 * MG;  // loads per stage and wave: codes, scales x 2, q x 2 x MG, d, s
-  static_assert(STG % 16 == 0 && S >= 2 && L * (S - 2) < 64 && R <= 64, "stage layout");
-  constexpr int RING = NW * S * STG, RED = NW * G * 2 * 16 * BQ * 4;
+  // With one row group (PS) the wave's weight scales are loaded once, before
+  // the ring starts, instead of with every stage.
+  constexpr bool PS = MG == 1;
+  constexpr int NB = kp_max_blocks(NW);  // blocks of the longest wave range
+  constexpr int SR = NB == 16 ? 17 : NB;  // scale row stride in 4-byte slots (rows on distinct banks)
+  constexpr int CB = R * 64, SB = PS ? 0 : 2 * R * 4, QB = 2 * BQ * 128 + 256, DB = BQ * 32;
+  constexpr int OQ = CB + SB, OD = OQ + QB;  // stage offsets of q and d
+  constexpr int STG = OD + 2 * DB;
+  constexpr int PSB = PS ? R * SR * 4 : 0;  // the preloaded scales
+  constexpr int WB = S * STG + PSB;         // LDS bytes per wave
+  constexpr int NCI = R / 16;               // code loads per stage (16 rows x 64 B each)
+  constexpr int L = NCI + (PS ? 0 : 2) + 2 * MG + 2 * MG;  // loads per stage: codes, scales, q, d + s
+  static_assert(STG % 16 == 0 && WB % 16 == 0 && S >= 2 && L * (S - 2) < 64 && R <= 64, "stage layout");
+  constexpr int RING = NW * WB, RED = NW * G * 2 * 16 * BQ * 4;
   __shared__ __attribute__((aligned(16))) uint8_t ring[RING > RED ? RING : RED];
 
   const int tid = threadIdx.x;
@@ -446,9 +461,27 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
   const int kw0 = nsc * w / NW, kw1 = nsc * (w + 1) / NW;
   const int niter = ((nsc + NW - 1) / NW + 1) / 2;  // every wave runs the longest range's stage count
 
-  uint8_t* rw = ring + w * (S * STG);
+  uint8_t* rw = ring + w * WB;
   const uint32_t ring0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)rw;  // LDS byte address
+  uint8_t* pre = rw + S * STG;  // the preloaded scales [R][SR] (4-byte slots)
+  const uint32_t pre0 = ring0 + S * STG;
+  // the wave's last block (a wave with none: block 0); stages past its range reload it
+  const int klast = kw1 > kw0 ? kw1 - 1 : 0;
+  const int bmax = kw1 > kw0 ? kw1 - kw0 - 1 : 0;  // last preloaded block, relative to kw0
 
+  // ---- the scale preload (issued before the first stage) ----
+  if constexpr (PS) {
+    // slot e: row e / SR, block kw0 + e % SR (past the range: its last block)
+#pragma unroll
+    for (int j = 0; j < (R * SR + 63) / 64; ++j) {
+      const int e = 64 * j + lane;
+      const int n = e / SR < R ? e / SR : R - 1;
+      const int b = e % SR < bmax ? e % SR : bmax;
+      const int nr = n0 + 16 * ((n >> 4) / G1) + (n & 15);
+      const int nc = nr < N ? nr : N - 1;
+      if (e < R * SR) lds_dma2(((n >> 4) % G1 ? a.up_scales : scales) + (size_t)nc * nsc + kw0 + b, pre0 + 256 * j);
+    }
+  }
   // ---- this lane's load sources (block offsets added per stage, clamped to the row) ----
   const uint8_t* csrc[NCI];  // codes: load j -> row 16 j + lane / 4, slot lane % 4
   int cblk[NCI];             // which of the stage's two blocks that slot holds
@@ -485,32 +518,31 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
     dsrc[mg] = a.d + (size_t)(a.m0 + m) * nsub + ((lane >> 3) & 3);
     s_src[mg] = a.s + (size_t)(a.m0 + m) * nsub + ((lane >> 3) & 3);
   }
-  // the wave's last block (a wave with none: block 0); stages past its range reload it
-  const int klast = kw1 > kw0 ? kw1 - 1 : 0;
   auto issue = [&](int it) {
     const int kb = kw0 + 2 * it;
     const uint32_t st = ring0 + (uint32_t)((it % S) * STG);
     auto blk_of = [&](int i) { return kb + i < klast ? kb + i : klast; };
 #pragma unroll
     for (int j = 0; j < NCI; ++j) lds_dma16(csrc[j] + (size_t)blk_of(cblk[j]) * 32, st + 1024 * j);
+    if constexpr (!PS)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        if (lane < R) lds_dma2(ssrc + blk_of(i), st + CB + i * R * 4);
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-      if (lane < R) lds_dma2(ssrc + blk_of(i), st + CB + i * R * 4);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int mg = 0; mg < MG; ++mg) lds_dma16(qsrc[mg] + (size_t)blk_of(i) * 128, st + CB + SB + (i * BQ + 8 * mg) * 128);
+      for (int mg = 0; mg < MG; ++mg) lds_dma16(qsrc[mg] + (size_t)blk_of(i) * 128, st + OQ + (i * BQ + 8 * mg) * 128);
 #pragma unroll
     for (int mg = 0; mg < MG; ++mg) {
-      lds_dma4(dsrc[mg] + 4 * blk_of(dblk), st + CB + SB + QB + 256 * mg);
-      lds_dma4(s_src[mg] + 4 * blk_of(dblk), st + CB + SB + QB + DB + 256 * mg);
+      lds_dma4(dsrc[mg] + 4 * blk_of(dblk), st + OD + 256 * mg);
+      lds_dma4(s_src[mg] + 4 * blk_of(dblk), st + OD + DB + 256 * mg);
     }
   };
 
   // the zero bytes after the q rows of every stage (no load writes them)
 #pragma unroll
   for (int s = 0; s < S; ++s)
-    if (lane < 16) *reinterpret_cast<u32x4*>(rw + s * STG + CB + SB + 2 * BQ * 128 + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
+    if (lane < 16) *reinterpret_cast<u32x4*>(rw + s * STG + OQ + 2 * BQ * 128 + 16 * lane) = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
   for (int it = 0; it < S - 1; ++it) issue(it);
 
@@ -524,15 +556,15 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
     for (int mg = 0; mg < MG; ++mg)
 #pragma unroll
       for (int P = 0; P < 2; ++P)
-        aoff[i][mg][P] = CB + SB + (holds ? (i * BQ + 8 * mg + x) * 128 + 16 * ((4 * P) ^ t ^ x)
-                                          : 2 * BQ * 128 + 16 * ((t & 1) ^ 1));
+        aoff[i][mg][P] = OQ + (holds ? (i * BQ + 8 * mg + x) * 128 + 16 * ((4 * P) ^ t ^ x)
+                                     : 2 * BQ * 128 + 16 * ((t & 1) ^ 1));
   int boff[2][2];  // code word 4P + t of block i of row li (group g adds 1024)
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int P = 0; P < 2; ++P) boff[i][P] = li * 64 + 16 * ((2 * i + P) ^ ((li >> 2) & 3)) + 4 * t;
   // d / s of output rows 4 (t & 1) .. + 3 of group mg, block i, sub-block 2P + (t >> 1): one 16-byte read
-  const int doff = CB + SB + QB + 4 * (8 * (t >> 1) + 4 * (t & 1));
+  const int dl = 4 * (8 * (t >> 1) + 4 * (t & 1));
 
   float acc[G][MG][4];
 #pragma unroll
@@ -549,6 +581,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
     if (kb >= kw1) continue;        // (wave-uniform; later iterations only wait and issue)
     const bool two = kb + 1 < kw1;  // (wave-uniform) the stage's second block is in the wave's range
     const uint8_t* st = rw + (it % S) * STG;
+    auto rel = [&](int i) { return (kb + i < klast ? kb + i : klast) - kw0; };  // preloaded block index
     // Per block: every LDS read first, then every MFMA into its own
     // registers, then the scaling, so that LDS and MFMA latencies overlap
     // instead of each product waiting for its own operands. A second block
@@ -565,15 +598,17 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
 #pragma unroll
         for (int mg = 0; mg < MG; ++mg) {
           A[P][mg] = *reinterpret_cast<const v4i*>(st + aoff[i][mg][P]);
-          const int o = doff + 256 * mg + 128 * i + 64 * P;
-          D[P][mg] = *reinterpret_cast<const u32x4*>(st + o);
-          C[P][mg] = *reinterpret_cast<const v4i*>(st + o + DB);
+          const uint8_t* o = st + OD + 256 * mg + 128 * i + 64 * P + dl;
+          D[P][mg] = *reinterpret_cast<const u32x4*>(o);
+          C[P][mg] = *reinterpret_cast<const v4i*>(o + DB);
         }
 #pragma unroll
         for (int g = 0; g < G; ++g) W[P][g] = *reinterpret_cast<const uint32_t*>(st + boff[i][P] + 1024 * g);
       }
 #pragma unroll
-      for (int g = 0; g < G; ++g) SC[g] = *reinterpret_cast<const uint16_t*>(st + CB + i * R * 4 + 4 * (16 * g + li));
+      for (int g = 0; g < G; ++g)
+        SC[g] = PS ? *reinterpret_cast<const uint16_t*>(pre + 4 * ((16 * g + li) * SR + rel(i)))
+                   : *reinterpret_cast<const uint16_t*>(st + CB + i * R * 4 + 4 * (16 * g + li));
       v4i I[2][G][MG];
 #pragma unroll
       for (int P = 0; P < 2; ++P) {
@@ -688,8 +723,6 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
 }
 
 // Two stages per wave (deeper rings measured no faster at M = 4, 8 and 16:
-// their LDS cost resident workgroups).
-// Two stages per wave (deeper rings measured no faster at M = 4, 8 and 16:
 // their LDS cost resident workgroups, and one wave per gate+up workgroup with
 // 2 to 8 stages took the same time for every depth).
 template <int NW, int MG, bool DUMP, int TR>
@@ -705,12 +738,20 @@ void by_mode_kp(int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
 
 // Waves per workgroup (the K split, so the outputs' summation order depends
 // on it; every caller of a shape gets the same): gate+up 2, K >= 8192 8,
-// else 4 (measured best of 2 / 4 / 8 at M = 4, 8, 16 on the 27B shapes).
+// else 4 (measured best of 2 / 4 / 8 at M = 4, 8, 16 on the 27B shapes),
+// and more where a wave's share would pass kp_max_blocks; 0: the shape is
+// longer than the packed tile takes.
+int kp_waves(int K, int mode) {
+  const int nsc = K / 128;
+  const int nw = mode == BTF_GEMV_SWIGLU ? (nsc <= 40 ? 2 : nsc <= 64 ? 4 : 8) : K >= 8192 ? 8 : 4;
+  return (nsc + nw - 1) / nw <= kp_max_blocks(nw) ? nw : 0;
+}
+
 template <int MG, bool DUMP, int TR = 1>
-void by_waves_kp(int K, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
-  if (mode == BTF_GEMV_SWIGLU)
+void by_waves_kp(int nw, int mode, const MfmaArgs& a, dim3 grid, hipStream_t st) {
+  if (nw == 2)
     by_mode_kp<2, MG, DUMP, TR>(mode, a, grid, st);
-  else if (K >= 8192)
+  else if (nw == 8)
     by_mode_kp<8, MG, DUMP, TR>(mode, a, grid, st);
   else
     by_mode_kp<4, MG, DUMP, TR>(mode, a, grid, st);
@@ -1236,17 +1277,18 @@ int gemm_mfma(const GemvSeg* segs, int nseg, int K, int m0, int nb, const Q8& ac
   if (ks) {
     // up to 16 rows with d and s 16-byte aligned (the LDS-direct loads of the
     // packed tile read them in 16-byte pieces): the packed tile
-    if (nb <= 16 && ((reinterpret_cast<uintptr_t>(act.d) | reinterpret_cast<uintptr_t>(act.s)) & 15) == 0) {
+    const int kw = kp_waves(K, mode);
+    if (nb <= 16 && kw && ((reinterpret_cast<uintptr_t>(act.d) | reinterpret_cast<uintptr_t>(act.s)) & 15) == 0) {
       const dim3 gk(tiles, 1);
       if (qout) {
         if (nb <= 8)
-          by_waves_kp<1, false, 2>(K, mode, a, gk, st);
+          by_waves_kp<1, false, 2>(kw, mode, a, gk, st);
         else
-          by_waves_kp<2, false, 2>(K, mode, a, gk, st);
+          by_waves_kp<2, false, 2>(kw, mode, a, gk, st);
       } else if (nb <= 8) {
-        dmp ? by_waves_kp<1, true>(K, mode, a, gk, st) : by_waves_kp<1, false>(K, mode, a, gk, st);
+        dmp ? by_waves_kp<1, true>(kw, mode, a, gk, st) : by_waves_kp<1, false>(kw, mode, a, gk, st);
       } else {
-        dmp ? by_waves_kp<2, true>(K, mode, a, gk, st) : by_waves_kp<2, false>(K, mode, a, gk, st);
+        dmp ? by_waves_kp<2, true>(kw, mode, a, gk, st) : by_waves_kp<2, false>(kw, mode, a, gk, st);
       }
       return launch_status("gemm_kp_kernel");
     }
