@@ -187,12 +187,13 @@ struct WorkRec {
   int t0, n, P, uq;  // uq = u0 | s0 << 8 | q0 << 16
 };
 struct OpRec {
-  int first, R, next, sq;  // sq = S | qlog << 8
+  int first, R, next, sq;  // sq = S | qlog << 8 | il << 16
 };
 constexpr int kRecSlots = 3;  // records of ops i, i + 1, i + 2 (slot = op index % 3)
 
 template <bool kFull>
 struct Lds {
+  static constexpr bool kPrepped = kFull;
   static constexpr int kCW = cw_of<kFull>();
   OpDev opd[kMaxOps];        // the program
   // An op's Q8 input (by op parity) as the image of its LL words: per
@@ -620,6 +621,7 @@ struct OpWork {
   int t0, n, P;        // the wave's first item, real items, entries (a multiple of kRing)
   int u0, s0, q0;      // (u, s, q) of item t0
   int R;               // rows of part[slice][.] (the workgroup's units x 4 * Qu)
+  int il;              // 1: unit-interleaved (the wave's batches are batch `wave` of each unit)
 };
 // Every field is assigned on every path (a partly assigned struct would be
 // kept in scratch memory, whose accesses count in vmcnt).
@@ -638,6 +640,26 @@ __device__ __forceinline__ OpWork op_work_calc(const LT& L, int nops, int wave, 
   w.R = (nunits << w.qlog) * 4;
   const int U = w.S << w.qlog;  // items per unit
   const int T = nunits * U;
+  // Plain programs, one batch per wave per unit (gate+up at 5120 columns:
+  // 5 slices x 16 quads): wave w takes batch w of every unit, in unit order,
+  // so that the workgroup's units complete one after the other (the I/O waves
+  // publish the first while the others are computed) instead of all at the
+  // op's end. A consumer then finds the units of the workgroups with one unit
+  // more than the rest late in one input slice, not in every slice that
+  // holds one of them. The wave's batches all read the same slice. (With
+  // prepped inputs the contiguous runs are kept: a wave with one slice holds
+  // all its batches behind that slice's prep, and the waves of the slice
+  // prepped last then finish last; measured 0.6 % slower per token.)
+  w.il = !LT::kPrepped && U == LT::kCW * kRing ? 1 : 0;
+  if (w.il) {
+    w.t0 = wave * kRing;
+    w.n = nunits * kRing;
+    w.P = (nunits > 0 ? nunits : 1) * kRing;
+    w.u0 = 0;
+    w.s0 = w.t0 >> w.qlog;
+    w.q0 = w.t0 & (Qu - 1);
+    return w;
+  }
   // Batches are spread evenly over the waves, floor(B / kCW) each, the
   // remaining B % kCW one more each, those first to the compute waves of
   // SIMDs 2 and 3 (wave v runs on SIMD v % 4; the I/O waves, the last two,
@@ -662,7 +684,7 @@ __device__ __forceinline__ OpWork op_work_calc(const LT& L, int nops, int wave, 
   w.n = t1 > w.t0 ? t1 - w.t0 : 0;
   w.P = (b1 > b0 ? b1 - b0 : 1) * kRing;
   const int ua = U ? w.t0 / U : 0, ra = w.t0 - ua * U;
-  w.u0 = ua;
+  w.u0 = ua;  // (w.il: 0 on this path)
   w.s0 = ra >> w.qlog;
   w.q0 = ra & (Qu - 1);
   return w;
@@ -677,7 +699,7 @@ __device__ __forceinline__ void stage_work(LT& L, int nops, int wg, int G, int i
     const OpWork w = op_work_calc(L, nops, iol, wg, G, i);
     const int slot = i % kRecSlots;
     L.wrec[slot][iol] = WorkRec{w.t0, w.n, w.P, w.u0 | (w.s0 << 8) | (w.q0 << 16)};
-    if (iol == 0) L.orec[slot] = OpRec{w.first, w.R, w.next, w.S | (w.qlog << 8)};
+    if (iol == 0) L.orec[slot] = OpRec{w.first, w.R, w.next, w.S | (w.qlog << 8) | (w.il << 16)};
   }
 }
 template <class LT>
@@ -699,7 +721,8 @@ __device__ __forceinline__ OpWork op_work(const LT& L, int wave, int i) {
   w.next = sgpr(o.next);
   const int sq = sgpr(o.sq);
   w.S = sq & 255;
-  w.qlog = sq >> 8;
+  w.qlog = (sq >> 8) & 255;
+  w.il = LT::kPrepped ? 0 : sq >> 16;  // (a constant in the prepped instance: no interleaved paths there)
   return w;
 }
 
@@ -712,7 +735,9 @@ __device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, i
   const int tl = w.t0 + w.n - 1;
   const int ub = tl / U, sb = (tl - ub * U) >> w.qlog;
   a0 = a1 = b0 = b1 = 0;
-  if (ub == w.u0) {
+  if (w.il) {  // unit-interleaved: every batch in slice s0
+    a0 = w.s0 * kWS, a1 = (w.s0 + 1) * kWS;
+  } else if (ub == w.u0) {
     a0 = w.s0 * kWS, a1 = (sb + 1) * kWS;
   } else if (ub == w.u0 + 1 && sb + 1 < w.s0) {
     a0 = w.s0 * kWS, a1 = w.S * kWS, b1 = (sb + 1) * kWS;
@@ -780,7 +805,11 @@ __device__ __forceinline__ LaneOff lane_off(const OpLd& d, int l16, int grp) {
 struct BPos {
   int u, s, qb;
 };
-__device__ __forceinline__ void bpos_next(int qlog, int S, BPos& p) {
+__device__ __forceinline__ void bpos_next(int qlog, int S, int il, BPos& p) {
+  if (il) {  // unit-interleaved: the same position of the next unit
+    ++p.u;
+    return;
+  }
   p.qb += kRing;
   if (p.qb == (1 << qlog)) {
     p.qb = 0;
@@ -1079,14 +1108,14 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
         // uniform value: LDS operations of a wave complete in order, so the
         // I/O waves see the partial sums once they see the count)
         asm volatile("" ::: "memory");
-        L.ucnt[wave][cp.u] = (uint32_t)(cur.t0 + (b + 1) * kRing - max(cur.t0, cp.u * U));
+        L.ucnt[wave][cp.u] = cur.il ? (uint32_t)kRing : (uint32_t)(cur.t0 + (b + 1) * kRing - max(cur.t0, cp.u * U));
       }
       if (!last && np.s != cp.s) load_act(L, ob, np.s, l16, aq, ad, an);
       cp = np;
     };
     for (int b = 0; b < nb - 1; ++b) {  // refills: the next batch of this op
       BPos np = cp;
-      bpos_next(cur.qlog, cur.S, np);
+      bpos_next(cur.qlog, cur.S, cur.il, np);
       run_batch(b, ld_cur, lo_cur, batch_addr(ld_cur, cur.first, G, np), np, false, (b + 1) * kRing < cur.n);
     }
     {
