@@ -392,7 +392,8 @@ def test_gemm_batched_and_prefill(hip, oracle, M):
     assert_close_1e3(host(y), ref, f"M={M}")
 
 
-@pytest.mark.parametrize("K,M", [(128, 3), (384, 17), (1152, 5), (3200, 32), (17536, 9)])
+@pytest.mark.parametrize("K,M", [(128, 3), (384, 17), (1152, 5), (3200, 32), (17536, 9), (6144, 5), (10240, 6),
+                                 (20608, 4)])
 def test_gemm_k_split_tile_edges(hip, oracle, K, M):
     """Batches of 3..32 rows run on the K-split 16-row tiles (each wave a
     contiguous share of the 128-column blocks: the packed tile up to 16 rows,
@@ -400,7 +401,10 @@ def test_gemm_k_split_tile_edges(hip, oracle, K, M):
     that do not split evenly (1 block: the other waves idle; 3, 9, 25, 137
     blocks: odd shares), one and two groups of activation rows with dead rows,
     16-row weight tiles with dead rows (N = 37, 9), and the three modes,
-    against the emulator GEMV."""
+    against the emulator GEMV. Up to 8 rows the packed tile loads each wave's
+    weight scales once: swiglu there takes 4 waves past 40 blocks (48 blocks:
+    K = 6144) and 8 past 64 (80 blocks: K = 10240), and shapes past 160
+    blocks (161: K = 20608) take the register-staged tile."""
     rng = np.random.default_rng(K + 1000 * M)
     _, q, d, s = random_act(oracle, rng, M, K, 3.0)
     act = q8_dev(q, d, s, hip)
