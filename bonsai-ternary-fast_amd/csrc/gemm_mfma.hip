@@ -404,15 +404,16 @@ __host__ __device__ constexpr int kp_max_blocks(int nw) { return nw == 4 ? 16 : 
 //     y = sum over waves w, in order, of (accE_w + accO_w).
 // Each wave streams its blocks two at a time through a private S-stage ring
 // of LDS-direct loads (no registers held by loads in flight): each code load
-// reads 64 contiguous bytes (two blocks) of each of 16 rows. With one row
-// group (MG = 1) the weight scales of the wave's whole range are loaded once,
+// reads 64 contiguous bytes (two blocks) of each of 16 rows. Where the LDS
+// allows (all but two swiglu instances, below) the weight scales of the
+// wave's whole range are loaded once,
 // before the first stage, into [R][SR] 4-byte slots after the ring: a stage
 // of 2 blocks then carries no scale loads (their HBM lines, apart from the
 // code rows, cost ~2.5 us of gate+up at M = 8 when every stage fetched its
 // own). Stages past the wave's range reload its last block (L2 hits, never
 // read back) to keep the per-stage load count. Stage layout (bytes): codes
 // [R][4 x 16 B] with chunk c of row n at slot c ^ ((n >> 2) & 3) (the 64
-// lanes' words then fall in 64 banks), scales [2][R] in 4-byte slots (MG = 2), q
+// lanes' words then fall in 64 banks), scales [2][R] in 4-byte slots (without the preload), q
 // [2][BQ][8 x 16 B] with chunk c of row r at slot c ^ (r & 7), then 256 zero
 // bytes (the A lanes that carry no data read one 16-byte chunk of them, on
 // banks that the data lanes of the same pass leave free), d
@@ -424,9 +425,12 @@ __global__ void __launch_bounds__(64 * NW) gemm_kp_kernel(MfmaArgs a) {
   constexpr int G = G1 * TR;  // 16-row groups: tile t, matrix g1 at t * G1 + g1
   constexpr int R = 16 * G;   // staged weight rows per wave
   constexpr int BQ = 8 * MG;  // activation rows
-  // With one row group (PS) the wave's weight scales are loaded once, before
-  // the ring starts, instead of with every stage.
-  constexpr bool PS = MG == 1;
+  // PS: the wave's weight scales are loaded once, before the ring starts,
+  // instead of with every stage. Not for swiglu with two row groups on 2
+  // waves of 16-row tiles (the preload would cost the fifth resident
+  // workgroup per CU that gate+up's 1088 need) or on 8 waves of 32-row tiles
+  // (past the 160 KB of LDS).
+  constexpr bool PS = MG == 1 || !(MODE == BTF_GEMV_SWIGLU && (TR == 1 ? NW == 2 : NW == 8));
   constexpr int NB = kp_max_blocks(NW);  // blocks of the longest wave range
   constexpr int SR = NB == 16 ? 17 : NB;  // scale row stride in 4-byte slots (rows on distinct banks)
   constexpr int CB = R * 64, SB = PS ? 0 : 2 * R * 4, QB = 2 * BQ * 128 + 256, DB = BQ * 32;
