@@ -987,11 +987,24 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
 #pragma unroll
     for (int r = 0; r < kRing; ++r) issue_entry(d0, l0, a, r, ring[r], w0.n > 0);
   }
-  // Per op, the input fetch holds only the op index and the ring across it:
-  // the op's work record and load parameters are read again from LDS after
-  // it (the scalar registers they would hold are what the prep needs).
+  // Per op, the op's work record and load parameters are read from LDS
+  // before the input wait: after it they would be LDS round trips on the op's
+  // critical path (measured: sweep 1.850 -> 1.810 ms, whole token 2.841 ->
+  // 2.788 ms). Plain programs also read the next op's there, for the last
+  // batch's refill (sweep 1.810 -> 1.794 ms); programs with preps read those
+  // in the last batch, as the scalar registers that would hold them across
+  // the op are what the prep needs. Op i + 1's records are staged by the I/O
+  // waves during op i - 1 and visible after that op's barrier B.
   for (int opi = first;;) {
     const int ob = opi & 1;  // LDS buffers of this op
+    const OpLd ld_pre = op_ld(L, opi);
+    const OpWork w_pre = op_work(L, wave, opi);
+    OpLd ld_nx;
+    OpWork w_nx;
+    if constexpr (!kFull) {  // and the next op's, which the last batch loads from
+      ld_nx = op_ld(L, w_pre.next < nops ? w_pre.next : opi);
+      w_nx = op_work(L, wave, w_pre.next);
+    }
     {
     // An input with a prep: the op's slices are shared out over the compute
     // waves (wave w takes slices w, w + kCW, ...), each slice prepped once
@@ -1021,7 +1034,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
         mine(std::false_type{});
       __builtin_amdgcn_s_setprio(0);
     }
-    const OpWork cur = op_work(L, wave, opi);
+    const OpWork cur = w_pre;
     if (cur.n > 0) {
       if (sgpr(L.opd[cur.i].early)) {
         // fetched by the I/O waves (early_seq only grows within a launch:
@@ -1064,8 +1077,8 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       }
     }
     }
-    OpLd ld_cur = op_ld(L, opi);  // (its reads first: in flight with op_work's)
-    const OpWork cur = op_work(L, wave, opi);
+    OpLd ld_cur = ld_pre;
+    const OpWork cur = w_pre;
     LaneOff lo_cur = lane_off(ld_cur, l16, grp);
     const int U = cur.S << cur.qlog;  // items per unit
     BPos cp{cur.u0, cur.s0, cur.q0};  // the batch being consumed
@@ -1121,11 +1134,11 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
     {
       // the last batch refills with the next op's first batch (past the
       // program's end: this op's matrices again). Its addresses are formed
-      // only here, so they hold no registers through the op's other batches.
-      // (read unconditionally -- past the program's end this op's own
-      // descriptor again -- so that no branch splits the reads)
-      ld_cur = op_ld(L, cur.next < nops ? cur.next : opi);
-      const OpWork nw = op_work(L, wave, cur.next);
+      // only here, so they hold no vector registers through the op's other
+      // batches. (read unconditionally -- past the program's end this op's
+      // own descriptor again -- so that no branch splits the reads)
+      ld_cur = kFull ? op_ld(L, cur.next < nops ? cur.next : opi) : ld_nx;
+      const OpWork nw = kFull ? op_work(L, wave, cur.next) : w_nx;
       lo_cur = lane_off(ld_cur, l16, grp);
       run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nw.first, G, BPos{nw.u0, nw.s0, nw.q0}), cp, true, nw.n > 0);
     }
