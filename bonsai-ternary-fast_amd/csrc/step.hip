@@ -768,18 +768,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* p) {
   // stride 0, 4 GB of records, 32-bit data format (raw buffer loads)
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, -1, 0x00020000);
 }
-template <class LT>
-__device__ __forceinline__ OpLd op_ld(const LT& L, int i) {
-  const OpDev& o = L.opd[i];
-  // Every field is read before any is tested, so the reads are in flight
-  // together (one LDS round trip; reading the up matrix only for a swiglu
-  // would make it a second, and this sits on the critical path of an op).
-  const int mode = sgpr(o.mode);
-  const uint8_t* c = sgpr_ptr(o.codes);
-  const uint16_t* sc = sgpr_ptr(o.scales);
-  const uint8_t* uc = sgpr_ptr(o.up_codes);
-  const uint16_t* us = sgpr_ptr(o.up_scales);
-  const uint32_t K = (uint32_t)sgpr(o.K), N = (uint32_t)sgpr(o.N);
+__device__ __forceinline__ OpLd make_ld(int mode, const uint8_t* c, const uint16_t* sc, const uint8_t* uc,
+                                       const uint16_t* us, uint32_t K, uint32_t N) {
   OpLd d;
   d.sw = mode == BTF_GEMV_SWIGLU;
   d.clo = rsrc(c);
@@ -791,6 +781,62 @@ __device__ __forceinline__ OpLd op_ld(const LT& L, int i) {
   d.lastc = (N - 4) * d.rowc;
   d.lasts = (N - 4) * d.rows;
   return d;
+}
+template <class LT>
+__device__ __forceinline__ OpLd op_ld(const LT& L, int i) {
+  const OpDev& o = L.opd[i];
+  // Every field is read before any is tested, so the reads are in flight
+  // together (one LDS round trip; reading the up matrix only for a swiglu
+  // would make it a second, and this sits on the critical path of an op).
+  return make_ld(sgpr(o.mode), sgpr_ptr(o.codes), sgpr_ptr(o.scales), sgpr_ptr(o.up_codes), sgpr_ptr(o.up_scales),
+                 (uint32_t)sgpr(o.K), (uint32_t)sgpr(o.N));
+}
+// What the loads of op i's first batch need -- its descriptor's matrix
+// fields, and the op's first unit and this wave's item count and position --
+// read from LDS into vector registers (uniform values, pinned there by empty
+// asms): a wave holds them through the op before, whose last batch issues
+// those loads, and forms the load parameters there with scalar reads of its
+// own registers instead of an LDS round trip. (In scalar registers they
+// would be spilled: the op's own parameters fill them.)
+struct NextRec {
+  int mode, K, N, first, n, uq;
+  uint32_t p[8];  // codes, scales, up_codes, up_scales (low, high words)
+};
+template <class LT>
+__device__ __forceinline__ NextRec next_rec(const LT& L, int wave, int di, int wi) {
+  const OpDev& o = L.opd[di];
+  NextRec r;
+  r.mode = o.mode;
+  r.K = o.K;
+  r.N = o.N;
+  const uint32_t* pc = reinterpret_cast<const uint32_t*>(&o.codes);
+  const uint32_t* ps = reinterpret_cast<const uint32_t*>(&o.scales);
+  const uint32_t* puc = reinterpret_cast<const uint32_t*>(&o.up_codes);
+  const uint32_t* pus = reinterpret_cast<const uint32_t*>(&o.up_scales);
+  for (int k = 0; k < 2; ++k) {
+    r.p[k] = pc[k];
+    r.p[2 + k] = ps[k];
+    r.p[4 + k] = puc[k];
+    r.p[6 + k] = pus[k];
+  }
+  const int slot = wi % kRecSlots;
+  r.first = L.orec[slot].first;
+  r.n = L.wrec[slot][wave].n;
+  r.uq = L.wrec[slot][wave].uq;
+  asm volatile("" : "+v"(r.mode), "+v"(r.K), "+v"(r.N), "+v"(r.first), "+v"(r.n), "+v"(r.uq));
+  asm volatile("" : "+v"(r.p[0]), "+v"(r.p[1]), "+v"(r.p[2]), "+v"(r.p[3]), "+v"(r.p[4]), "+v"(r.p[5]),
+               "+v"(r.p[6]), "+v"(r.p[7]));
+  return r;
+}
+template <class T>
+__device__ __forceinline__ T* sgpr_ptr2(uint32_t lo, uint32_t hi) {  // (each half unsigned: no sign extension)
+  const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane(lo), h = (uint32_t)__builtin_amdgcn_readfirstlane(hi);
+  return reinterpret_cast<T*>(((uint64_t)h << 32) | l);
+}
+__device__ __forceinline__ OpLd next_ld(const NextRec& r) {
+  return make_ld(sgpr(r.mode), sgpr_ptr2<const uint8_t>(r.p[0], r.p[1]), sgpr_ptr2<const uint16_t>(r.p[2], r.p[3]),
+                 sgpr_ptr2<const uint8_t>(r.p[4], r.p[5]), sgpr_ptr2<const uint16_t>(r.p[6], r.p[7]),
+                 (uint32_t)sgpr(r.K), (uint32_t)sgpr(r.N));
 }
 // This lane's part of an entry's offsets: row grp of the quad, chunk l16 of
 // the slice (16 code bytes; the fp16 scale of its 128-column block).
@@ -990,21 +1036,18 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
   // Per op, the op's work record and load parameters are read from LDS
   // before the input wait: after it they would be LDS round trips on the op's
   // critical path (measured: sweep 1.850 -> 1.810 ms, whole token 2.841 ->
-  // 2.788 ms). Plain programs also read the next op's there, for the last
-  // batch's refill (sweep 1.810 -> 1.794 ms); programs with preps read those
-  // in the last batch, as the scalar registers that would hold them across
-  // the op are what the prep needs. Op i + 1's records are staged by the I/O
-  // waves during op i - 1 and visible after that op's barrier B.
+  // 2.788 ms). Plain programs also read the next op's there (into vector
+  // registers, NextRec), for the last batch's refill (sweep 1.810 -> 1.794
+  // ms); programs with preps read those in the last batch, as the registers
+  // that would hold them across the op are what the prep needs. Op i + 1's
+  // records are staged by the I/O waves during op i - 1 and visible after
+  // that op's barrier B.
   for (int opi = first;;) {
     const int ob = opi & 1;  // LDS buffers of this op
     const OpLd ld_pre = op_ld(L, opi);
     const OpWork w_pre = op_work(L, wave, opi);
-    OpLd ld_nx;
-    OpWork w_nx;
-    if constexpr (!kFull) {  // and the next op's, which the last batch loads from
-      ld_nx = op_ld(L, w_pre.next < nops ? w_pre.next : opi);
-      w_nx = op_work(L, wave, w_pre.next);
-    }
+    NextRec nx;  // plain programs: the next op's, which the last batch loads from
+    if constexpr (!kFull) nx = next_rec(L, wave, w_pre.next < nops ? w_pre.next : opi, w_pre.next);
     {
     // An input with a prep: the op's slices are shared out over the compute
     // waves (wave w takes slices w, w + kCW, ...), each slice prepped once
@@ -1137,10 +1180,22 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       // only here, so they hold no vector registers through the op's other
       // batches. (read unconditionally -- past the program's end this op's
       // own descriptor again -- so that no branch splits the reads)
-      ld_cur = kFull ? op_ld(L, cur.next < nops ? cur.next : opi) : ld_nx;
-      const OpWork nw = kFull ? op_work(L, wave, cur.next) : w_nx;
+      int nfirst, nn, nuq;
+      if constexpr (kFull) {
+        ld_cur = op_ld(L, cur.next < nops ? cur.next : opi);
+        const OpWork nw = op_work(L, wave, cur.next);
+        nfirst = nw.first;
+        nn = nw.n;
+        nuq = nw.u0 | nw.s0 << 8 | nw.q0 << 16;
+      } else {
+        ld_cur = next_ld(nx);
+        nfirst = sgpr(nx.first);
+        nn = sgpr(nx.n);
+        nuq = sgpr(nx.uq);
+      }
       lo_cur = lane_off(ld_cur, l16, grp);
-      run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nw.first, G, BPos{nw.u0, nw.s0, nw.q0}), cp, true, nw.n > 0);
+      run_batch(nb - 1, ld_cur, lo_cur, batch_addr(ld_cur, nfirst, G, BPos{nuq & 255, (nuq >> 8) & 255, nuq >> 16}), cp,
+                true, nn > 0);
     }
     if constexpr (kFull) __builtin_amdgcn_s_setprio(0);
     lds_barrier();  // B: every wave is done with the op
