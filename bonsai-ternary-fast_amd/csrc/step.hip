@@ -1141,6 +1141,24 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
         if (b * kRing < cur.n) __builtin_amdgcn_s_setprio(1);
         else __builtin_amdgcn_s_setprio(0);
       }
+      if (!kFull && cur.n == 0) {
+        // Plain programs, a wave without items of the op: its refills (the
+        // next op's first batch) paced ~770 cycles apart instead of behind a
+        // dummy batch's dot products, which took issue slots from the real
+        // batches on the same SIMD (sweep -0.4 to -0.8 %). Issued back to
+        // back they queue in front of the op's real loads (1.828 ms); paced
+        // past the op's length, they hold barrier B (~1540 cycles apart:
+        // 1.914 ms). With preps the dummy batch stays: an idle wave there may
+        // have prepped slices first, and paced refills then outlast the op
+        // (2.806 against 2.779 ms per token).
+#pragma unroll
+        for (int r = 0; r < kRing; ++r) {
+          issue_entry(ld, lo, a, r, ring[r], real);
+          __builtin_amdgcn_s_sleep(12);
+        }
+        cp = np;
+        return;
+      }
       float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
