@@ -650,11 +650,18 @@ __device__ __forceinline__ OpWork op_work_calc(const LT& L, int nops, int wave, 
   // prepped inputs the contiguous runs are kept: a wave with one slice holds
   // all its batches behind that slice's prep, and the waves of the slice
   // prepped last then finish last; measured 0.6 % slower per token.)
-  w.il = !LT::kPrepped && U == LT::kCW * kRing ? 1 : 0;
+  // With 10 compute waves (il = 2) SIMDs 0 and 1 hold three of them and
+  // SIMDs 2 and 3 two (beside the I/O waves), so in every odd unit the
+  // batches of positions 8 and 9 go to waves 2 and 3 instead of waves 8 and
+  // 9: each SIMD then runs 5 batches per two units, not 6 / 6 / 4 / 4
+  // (sweep 1.789 -> 1.783 ms over 6 alternating A/B pairs, bit-exact).
+  w.il = !LT::kPrepped && U == LT::kCW * kRing ? (LT::kCW == 10 ? 2 : 1) : 0;
   if (w.il) {
+    const int cnt = w.il == 2 && (wave == 2 || wave == 3) ? nunits + nunits / 2
+                    : w.il == 2 && (wave == 8 || wave == 9) ? (nunits + 1) / 2 : nunits;
     w.t0 = wave * kRing;
-    w.n = nunits * kRing;
-    w.P = (nunits > 0 ? nunits : 1) * kRing;
+    w.n = cnt * kRing;
+    w.P = (cnt > 0 ? cnt : 1) * kRing;
     w.u0 = 0;
     w.s0 = w.t0 >> w.qlog;
     w.q0 = w.t0 & (Qu - 1);
@@ -729,7 +736,7 @@ __device__ __forceinline__ OpWork op_work(const LT& L, int wave, int i) {
 // The input slices the wave's real items read, as input LL word ranges
 // [a0, a1) and [b0, b1) (one of them, or both, may be empty): the items run
 // from (u0, s0) to the last one's (ub, sb).
-__device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, int& b0, int& b1) {
+__device__ __forceinline__ void input_words(const OpWork& w, int wave, int& a0, int& a1, int& b0, int& b1) {
   constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
   const int U = w.S << w.qlog;
   const int tl = w.t0 + w.n - 1;
@@ -737,6 +744,10 @@ __device__ __forceinline__ void input_words(const OpWork& w, int& a0, int& a1, i
   a0 = a1 = b0 = b1 = 0;
   if (w.il) {  // unit-interleaved: every batch in slice s0
     a0 = w.s0 * kWS, a1 = (w.s0 + 1) * kWS;
+    if (w.il == 2 && (wave == 2 || wave == 3)) {  // and the slice of its extra position (odd units)
+      const int s2 = ((wave + 6) * kRing) >> w.qlog;
+      b0 = s2 * kWS, b1 = (s2 + 1) * kWS;
+    }
   } else if (ub == w.u0) {
     a0 = w.s0 * kWS, a1 = (sb + 1) * kWS;
   } else if (ub == w.u0 + 1 && sb + 1 < w.s0) {
@@ -851,7 +862,19 @@ __device__ __forceinline__ LaneOff lane_off(const OpLd& d, int l16, int grp) {
 struct BPos {
   int u, s, qb;
 };
-__device__ __forceinline__ void bpos_next(int qlog, int S, int il, BPos& p) {
+__device__ __forceinline__ void bpos_next(int qlog, int S, int il, int wave, BPos& p) {
+  if (il == 2) {  // balanced unit-interleaved (10 compute waves)
+    const int tb = wave * kRing, te = tb + 6 * kRing;  // the wave's position and, in odd units, its extra one
+    if ((wave == 2 || wave == 3) && (p.u & 1) && p.s == (tb >> qlog)) {
+      p.s = te >> qlog;
+      p.qb = te & ((1 << qlog) - 1);
+    } else {
+      p.u += (wave == 8 || wave == 9) ? 2 : 1;
+      p.s = tb >> qlog;
+      p.qb = tb & ((1 << qlog) - 1);
+    }
+    return;
+  }
   if (il) {  // unit-interleaved: the same position of the next unit
     ++p.u;
     return;
@@ -1096,7 +1119,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
         asm volatile("" ::: "memory");
       } else {
         int a0, a1, b0w, b1w;
-        input_words(cur, a0, a1, b0w, b1w);
+        input_words(cur, wave, a0, a1, b0w, b1w);
         if (pi >= 0) {  // wait for the prepped slices this wave's items read
           constexpr int kWS = 32 * kWordsPerBlock;  // input words per slice
           const int s1 = a0 / kWS, n1 = a1 / kWS - s1, s2 = b0w / kWS, n = n1 + b1w / kWS - s2;
@@ -1182,14 +1205,16 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
         // uniform value: LDS operations of a wave complete in order, so the
         // I/O waves see the partial sums once they see the count)
         asm volatile("" ::: "memory");
-        L.ucnt[wave][cp.u] = cur.il ? (uint32_t)kRing : (uint32_t)(cur.t0 + (b + 1) * kRing - max(cur.t0, cp.u * U));
+        // (il = 2: a wave's extra batch of an odd unit counts both of its batches)
+        L.ucnt[wave][cp.u] = cur.il ? (uint32_t)(cur.il == 2 && cp.s != cur.s0 ? 2 * kRing : kRing)
+                                    : (uint32_t)(cur.t0 + (b + 1) * kRing - max(cur.t0, cp.u * U));
       }
       if (!last && np.s != cp.s) load_act(L, ob, np.s, l16, aq, ad, an);
       cp = np;
     };
     for (int b = 0; b < nb - 1; ++b) {  // refills: the next batch of this op
       BPos np = cp;
-      bpos_next(cur.qlog, cur.S, cur.il, np);
+      bpos_next(cur.qlog, cur.S, cur.il, wave, np);
       run_batch(b, ld_cur, lo_cur, batch_addr(ld_cur, cur.first, G, np), np, false, (b + 1) * kRing < cur.n);
     }
     {
