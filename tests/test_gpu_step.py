@@ -426,6 +426,56 @@ class Sweep27B:
         return np.ascontiguousarray(codes), np.ascontiguousarray(scales)
 
 
+@pytest.mark.parametrize("NF", [4096, 9216, 17408])
+def test_step_work_orders_bit_exact(hip, NF):
+    """The plain kernel's work orders, at 5120 columns: a swiglu op of NF
+    outputs (128, 288 or 544 units over 256 workgroups: 0-1, 1-2 or 2-3
+    units per workgroup) runs the unit-interleaved order rebalanced over the
+    SIMDs (in odd units waves 2 and 3 take the batches of positions 8 and 9,
+    waves 8 and 9 skip them; with one unit there is no odd unit), then an
+    add op of K = NF and two store ops of 5 and 7 batches per unit-owning
+    workgroup (the extra batches on the lowest waves, the waves without
+    items pacing their refills). Two layers, every vector bit-exact against
+    the same chain launched op by op."""
+    torch = _torch()
+    G = hip.GemvMode
+    E, N2 = 5120, 7168
+    rng = np.random.default_rng(NF)
+    res0 = rng.standard_normal(E).astype(np.float32)
+    mats = {}
+    mid = 0
+    for l in range(2):
+        for name, N, K in (("gate", NF, E), ("up", NF, E), ("down", E, NF), ("s5", N2, E), ("s7", 1792, 7 * 1024)):
+            mats[(name, l)] = gen_dev_mat(hip, N, K, 900 + mid, seed=NF)
+            mid += 1
+    ops = []
+    for l in range(2):
+        g, u, d, a, b = (mats[(n, l)] for n in ("gate", "up", "down", "s5", "s7"))
+        ops += [hip.StepGemv(G.kSwiglu, E, NF, g.codes, g.scales, 0, 1, u.codes, u.scales),
+                hip.StepGemv(G.kAdd, NF, E, d.codes, d.scales, 1, 0),
+                hip.StepGemv(G.kStore, E, N2, a.codes, a.scales, 0, 2),
+                hip.StepGemv(G.kStore, 7 * 1024, 1792, b.codes, b.scales, 2, 3)]
+
+    def vectors():
+        t = [dev(res0), torch.zeros(NF, dtype=torch.float32, device="cuda"),
+             torch.zeros(N2, dtype=torch.float32, device="cuda"), torch.zeros(1792, dtype=torch.float32, device="cuda")]
+        return [hip.StepVec(int(v.numel()), v) for v in t], t
+
+    vecs, t = vectors()
+    prog = hip.StepProgram(vecs, ops)
+    prog.launch(stream())
+    torch.cuda.synchronize()
+    assert prog.error() == 0
+    _, s = vectors()
+    run_sequential(hip, ops, s)
+    for k, (a, b) in enumerate(zip(t, s)):
+        ga, gb = host(a), host(b)
+        assert np.isfinite(ga).all(), k
+        assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32)), \
+            f"vector {k}: step != sequential (max diff {np.max(np.abs(ga - gb)):.3e})"
+    prog.close()
+
+
 def test_step_27b_full_sweep_and_output_head(hip, oracle):
     """The benchmark's full decode-step program (config 5): 64 layers of the
     27B shapes plus the 5120->248320 output projection, 257 GEMVs in one
