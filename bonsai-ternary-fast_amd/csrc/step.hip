@@ -604,9 +604,9 @@ typedef const __attribute__((address_space(1))) _Float16 gf16;
 // 32*(j >> 4) + (j & 15), up row j 16 further).
 struct Slot {
   u32x4 c;
-  uint32_t s;  // the aligned word holding the fp16 scale of the chunk's 128-column block (a
-               // full word: the compiler cannot pack two slots' scales into one register,
-               // which would make it wait for a refill right after issuing it)
+  uint32_t s;  // the fp16 scale of the chunk's 128-column block, loaded as 16 bits and
+               // zero-extended into a full register (two slots' scales packed into one
+               // register would make the compiler wait for a refill right after issuing it)
 };
 
 // The items of an op are cut into batches of kRing, and each compute wave
@@ -862,7 +862,9 @@ struct LaneOff {
   uint32_t c, s;
 };
 __device__ __forceinline__ LaneOff lane_off(const OpLd& d, int l16, int grp) {
-  return LaneOff{(uint32_t)grp * d.rowc + (uint32_t)l16 * 16u, (uint32_t)grp * d.rows + (uint32_t)(l16 >> 2) * 4u};
+  // (the lane's scale: the fp16 of 128-column block l16 / 2, 16 bits loaded directly: no shift to
+  // its half of a word when it is consumed; sweep -0.55 %, whole token -0.7 %)
+  return LaneOff{(uint32_t)grp * d.rowc + (uint32_t)l16 * 16u, (uint32_t)grp * d.rows + (uint32_t)(l16 >> 1) * 2u};
 }
 
 // Position of a batch in the op's items: local unit, slice, first quad.
@@ -926,7 +928,7 @@ __device__ __forceinline__ void issue_entry(const OpLd& d, const LaneOff& lo, co
   const uint32_t os = min(a.os + dr * d.rows, a.ms);
   const __amdgpu_buffer_rsrc_t z = __builtin_amdgcn_make_buffer_rsrc((void*)0, (short)0, 0, 0x00020000);
   sl.c = __builtin_amdgcn_raw_buffer_load_b128(real ? (hi ? d.chi : d.clo) : z, (int)lo.c, (int)oc, kNT);
-  sl.s = __builtin_amdgcn_raw_buffer_load_b32(real ? (hi ? d.shi : d.slo) : z, (int)lo.s, (int)os, kNT);
+  sl.s = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(real ? (hi ? d.shi : d.slo) : z, (int)lo.s, (int)os, kNT);
 }
 
 // The activation of this lane's chunk of slice s (64 columns = two Q8
@@ -990,11 +992,10 @@ struct Consumed {
   int y0, y1;
   float f;
 };
-// hsh: 16 for a lane whose scale is the high half of its word (odd 128-column block), else 0
-__device__ __forceinline__ Consumed consume(const Slot& sl, uint32_t hsh, const uint32_t (&aq)[16], const int (&an)[2]) {
+__device__ __forceinline__ Consumed consume(const Slot& sl, const uint32_t (&aq)[16], const int (&an)[2]) {
   Consumed r;
   const u32x4 wv = sl.c;
-  r.f = h2f((uint16_t)(sl.s >> hsh));
+  r.f = h2f((uint16_t)sl.s);
   chunk_dot16(wv, aq, an, r.y0, r.y1);
   asm volatile("" : "+v"(r.f), "+v"(r.y0), "+v"(r.y1));
   return r;
@@ -1053,7 +1054,6 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
   const int l16 = lane & 15, grp = lane >> 4;
   const bool b0 = (lane & 1) != 0, b1 = (lane & 2) != 0;
   const bool sum_lane = sum_lanes(l16);
-  const uint32_t hsh = (uint32_t)((l16 >> 1) & 1) * 16u;
   Slot ring[kRing];
   {
     const OpWork w0 = op_work(L, wave, first);
@@ -1192,7 +1192,7 @@ __device__ __forceinline__ void compute_waves(Lds<kFull>& L, int nops, int first
       float v[kRing];
 #pragma unroll
       for (int r = 0; r < kRing; ++r) {
-        const Consumed c = consume(ring[r], hsh, aq, an);
+        const Consumed c = consume(ring[r], aq, an);
         __builtin_amdgcn_sched_barrier(0);
         issue_entry(ld, lo, a, r, ring[r], real);
         __builtin_amdgcn_sched_barrier(0);
