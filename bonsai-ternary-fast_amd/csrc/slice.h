@@ -71,9 +71,16 @@ __device__ __forceinline__ void xstage(float (&v)[16], int lane) {
     constexpr int kBit = X == 1 ? 0 : X == 2 ? 1 : X == 4 ? 2 : 3;
     const uint32_t flip = ((uint32_t)lane >> kBit & 1u) << 31;  // the upper lane negates its own value
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float p = lane_xor<X>(v[i]);
-      v[i] = p + __uint_as_float(__float_as_uint(v[i]) ^ flip);
+    // Four values at a time: each flip is written two or more instructions
+    // before the DPP add that reads it, so no wait states go between them
+    // (one at a time the compiler reused one register for every flip, with
+    // an s_nop before each add; whole token 2.766 -> 2.717 ms).
+    for (int i = 0; i < 16; i += 4) {
+      float t[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) t[k] = __uint_as_float(__float_as_uint(v[i + k]) ^ flip);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) v[i + k] = lane_xor<X>(v[i + k]) + t[k];
     }
   } else {
     static_assert(X == 16 || X == 32, "cross-row stages");
