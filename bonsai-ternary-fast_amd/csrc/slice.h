@@ -67,35 +67,52 @@ __device__ __forceinline__ void pair32(float v, float& lo, float& hi) {
 //    swaps, an add and a subtract per two entries.
 template <int X>
 __device__ __forceinline__ void xstage(float (&v)[16], int lane) {
+  // Four values (two pairs) at a time: each value a DPP or permlane
+  // instruction reads is written two or more instructions before it, so no
+  // wait states go between them (one value at a time, the compiler reused one
+  // register for every flip and put an s_nop before each read of it; whole
+  // token 2.766 -> 2.717 ms). The l ^ 4 stage issues its four mirror moves
+  // before the quad permutes that read them, and the cross-row stages swap two
+  // pairs before adding either, for the same reason (2.716 -> 2.711 ms).
   if constexpr (X <= 8) {
     constexpr int kBit = X == 1 ? 0 : X == 2 ? 1 : X == 4 ? 2 : 3;
     const uint32_t flip = ((uint32_t)lane >> kBit & 1u) << 31;  // the upper lane negates its own value
 #pragma unroll
-    // Four values at a time: each flip is written two or more instructions
-    // before the DPP add that reads it, so no wait states go between them
-    // (one at a time the compiler reused one register for every flip, with
-    // an s_nop before each add; whole token 2.766 -> 2.717 ms).
     for (int i = 0; i < 16; i += 4) {
       float t[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) t[k] = __uint_as_float(__float_as_uint(v[i + k]) ^ flip);
+      if constexpr (X == 4) {  // l ^ 4 = (l ^ 7) ^ 3: the mirror of all four first
+        float m[4];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) v[i + k] = lane_xor<X>(v[i + k]) + t[k];
+        for (int k = 0; k < 4; ++k) m[k] = dpp_f<0x141>(v[i + k]);
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[i + k] = dpp_f<0x1B>(m[k]) + t[k];
+      } else {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[i + k] = lane_xor<X>(v[i + k]) + t[k];
+      }
     }
   } else {
     static_assert(X == 16 || X == 32, "cross-row stages");
+    auto swap = [](float a, float b, float& lo, float& hi) {
+      const auto r = X == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false)
+                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+      lo = __uint_as_float(r[0]);
+      hi = __uint_as_float(r[1]);
+    };
 #pragma unroll
-    for (int i = 0; i < 16; i += 2) {
-      const auto r = X == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 1]),
-                                                                false, false)
-                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(v[i]), __float_as_uint(v[i + 1]),
-                                                                false, false);
-      const float lo = __uint_as_float(r[0]), hi = __uint_as_float(r[1]);
-      const float sum = lo + hi, dif = lo - hi;
-      const auto t = X == 16 ? __builtin_amdgcn_permlane16_swap(__float_as_uint(sum), __float_as_uint(dif), false, false)
-                             : __builtin_amdgcn_permlane32_swap(__float_as_uint(sum), __float_as_uint(dif), false, false);
-      v[i] = __uint_as_float(t[0]);
-      v[i + 1] = __uint_as_float(t[1]);
+    for (int i = 0; i < 16; i += 4) {
+      float lo[2], hi[2], sm[2], df[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) swap(v[i + 2 * k], v[i + 2 * k + 1], lo[k], hi[k]);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        sm[k] = lo[k] + hi[k];
+        df[k] = lo[k] - hi[k];
+      }
+#pragma unroll
+      for (int k = 0; k < 2; ++k) swap(sm[k], df[k], v[i + 2 * k], v[i + 2 * k + 1]);
     }
   }
 }
