@@ -1426,8 +1426,12 @@ __device__ __forceinline__ void wait_readers(int war_op, const uint32_t* prog, i
 // Row lr's partial sums over the op's S slices, added in slice order. The
 // loads go out in groups of kSumGroup before their adds (addresses clamped to
 // slice S - 1; a slice past S adds -0.0f, which leaves every sum as it is,
-// -0.0f included): at K = 17408 two LDS round trips instead of 17.
-constexpr int kSumGroup = 10;
+// -0.0f included): at K = 5120 one LDS round trip with no padded load, at
+// K = 17408 four instead of 17. (Groups of 10, five padded loads in every
+// 5-slice sum: sweep 1.752 and whole token 2.722 ms against 1.740 and 2.690;
+// groups of 6 and 8 in between, 17 slower still; groups of 3 and 4: 1.756
+// and 1.762.)
+constexpr int kSumGroup = 5;
 template <class LT>
 __device__ __forceinline__ float slice_sum(const LT& L, int S, int R, int lr) {
   float sum = 0.f;
